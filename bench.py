@@ -1,0 +1,280 @@
+"""Benchmark: weight-stream GB/s (% of HBM peak) and decode tok/s of the quantized-weight path,
+Llama-3-8B Q4_K_M layer shapes, B = 1 (the headline value) and B = 8.
+
+A step is one decode token's pass over the linear layers of all 32 layers of a random-init
+Llama-3-8B-shaped model in Q4_K_M: per layer norm+quantize, q/k/v in one launch, quantize,
+o (+residual), norm+quantize, gate+up+SiLU-GLU in one launch, quantize, down (+residual),
+exactly as leat's decode step calls them (leat/model.py:497-558 via leat/ops.py:23-55). Weights
+are 32 distinct layers of seeded synthetic blocks (4.41 GB, far beyond the 256 MB MALL), resident
+in HBM before the timed region; each step is one HIP-graph replay. `value` is weight bytes per
+step / step time, as leat's bench counts weight GB/s (leat/bench.py:71-82). The roofline object is
+for the dominant kernel (gate+up GLU matvec), timed with HIP events around each of its launches;
+the CPU baseline is the C restatement of leat's LEAT_KERNELS=ref product (oracle/leat_ref.c) on
+the host cores, over a bounded sample.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HIDDEN, FFN, KV, LAYERS = 4096, 14336, 1024, 32
+Q4_K, Q6_K = 12, 14
+HBM_PEAK_GBS = 8000.0
+METRIC = "weight-stream GB/s (% HBM peak) + decode tok/s, Llama-3-8B Q4_K_M shape, B=1/8"
+# (name, type, rows, cols) of a layer's matrices (config 2 of the benchmark)
+MATRICES = [
+    ("q", Q4_K, HIDDEN, HIDDEN), ("k", Q4_K, KV, HIDDEN), ("v", Q4_K, KV, HIDDEN),
+    ("o", Q4_K, HIDDEN, HIDDEN), ("gate", Q4_K, FFN, HIDDEN), ("up", Q4_K, FFN, HIDDEN),
+    ("down", Q6_K, HIDDEN, FFN),
+]  # fmt: skip
+BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def nbytes(t, rows, cols):
+    el, by = BLOCK[t]
+    return rows * cols // el * by
+
+
+LAYER_BYTES = sum(nbytes(t, r, c) for _, t, r, c in MATRICES)  # 137,822,208
+
+
+def synthetic_weights(torch, t, rows, cols, gen, device):
+    # uniform bytes; Q4_K d = f16(|N|*0.002), dmin = f16(|N|*0.001); Q6_K d = f16(|N|*0.002)
+    el, by = BLOCK[t]
+    n = rows * cols // el
+    blocks = torch.randint(0, 256, (n, by), dtype=torch.uint8, device=device, generator=gen)
+    def f16_field(scale):
+        v = (torch.randn(n, device=device, generator=gen).abs() * scale).half()
+        return v.view(torch.uint8).view(n, 2)
+    if t == Q4_K:
+        blocks[:, 0:2] = f16_field(0.002)
+        blocks[:, 2:4] = f16_field(0.001)
+    else:
+        blocks[:, 208:210] = f16_field(0.002)
+    return blocks
+
+
+class Step:
+    """Static buffers and the launch sequence of one decode step at B tokens."""
+
+    def __init__(self, torch, lib, layers, tokens, device):
+        self.torch, self.lib, self.layers, self.B = torch, lib, layers, tokens
+        f32 = dict(dtype=torch.float32, device=device)
+        i32 = dict(dtype=torch.int32, device=device)
+        B = tokens
+        gen = torch.Generator(device=device).manual_seed(1)
+        self.x = [torch.randn(B, HIDDEN, generator=gen, **f32) for _ in range(2)]
+        self.norm_w = torch.rand(HIDDEN, generator=gen, **f32) + 0.5
+        self.q8 = {n: (torch.empty(B * n // 4, **i32), torch.empty(B * n // 32, **f32), torch.empty(B * n // 32, **f32))
+                   for n in (HIDDEN, FFN)}  # fmt: skip
+        self.q8b = tuple(torch.empty_like(t) for t in self.q8[HIDDEN])
+        self.qkv = [torch.empty(B * r, **f32) for _, _, r, _ in MATRICES[:3]]
+        self.h = torch.empty(B, HIDDEN, **f32)
+        self.g = torch.empty(B, FFN, **f32)
+        self.glu_events = []
+
+    def quantize(self, x, n, out, norm):
+        q, d, s = out
+        w, eps = (self.norm_w.data_ptr(), 1e-5) if norm else (None, 0.0)
+        _call(self.lib, "leat_quantize_q8", x.data_ptr(), self.B, n, w, eps, q.data_ptr(), d.data_ptr(),
+              s.data_ptr(), self._stream())  # fmt: skip
+
+    def _stream(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def run(self, time_glu=False):
+        torch, lib, B = self.torch, self.lib, self.B
+        st = self._stream()
+        for i, w in enumerate(self.layers):
+            x, x_next = self.x[i % 2], self.x[(i + 1) % 2]
+            xq, xd, xs = self.q8[HIDDEN]
+            self.quantize(x, HIDDEN, self.q8[HIDDEN], True)
+            types = (ctypes.c_int * 3)(Q4_K, Q4_K, Q4_K)
+            ptrs = (ctypes.c_void_p * 3)(*[w[n].data_ptr() for n in ("q", "k", "v")])
+            rows = (ctypes.c_int * 3)(HIDDEN, KV, KV)
+            outs = (ctypes.c_void_p * 3)(*[o.data_ptr() for o in self.qkv])
+            _call(lib, "leat_matvecs", 3, types, ptrs, rows, HIDDEN, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
+                  B, outs, st)  # fmt: skip
+            # the attention output stands in with q's product: same shape, realistic values
+            aq, ad, as_ = self.q8b
+            self.quantize(self.qkv[0], HIDDEN, self.q8b, False)
+            _call(lib, "leat_matvec", Q4_K, w["o"].data_ptr(), HIDDEN, HIDDEN, aq.data_ptr(), ad.data_ptr(),
+                  as_.data_ptr(), B, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
+            self.quantize(self.h, HIDDEN, self.q8[HIDDEN], True)
+            if time_glu:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[0].record()
+            _call(lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
+                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), st)  # fmt: skip
+            if time_glu:
+                ev[1].record()
+                self.glu_events.append(ev)
+            gq, gd, gs = self.q8[FFN]
+            self.quantize(self.g, FFN, self.q8[FFN], False)
+            _call(lib, "leat_matvec", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, gq.data_ptr(), gd.data_ptr(),
+                  gs.data_ptr(), B, self.h.data_ptr(), x_next.data_ptr(), st)  # fmt: skip
+
+
+def _call(lib, name, *args):
+    if getattr(lib, name)(*args) != 0:
+        raise RuntimeError(f"{name}: {lib.leat_last_error().decode()}")
+
+
+def glu_bytes(B):
+    # algorithmic bytes of one gate+up GLU launch: both matrices, q8 activations (int8 + d + s),
+    # f32 outputs
+    return 2 * nbytes(Q4_K, FFN, HIDDEN) + B * (HIDDEN + HIDDEN // 32 * 8) + B * FFN * 4
+
+
+def measure(torch, lib, layers, B, steps, warmup, device):
+    step = Step(torch, lib, layers, B, device)
+    step.run()  # eager once: checks every launch
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.run()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    # the dominant kernel, timed by events around each of its launches (eager steps)
+    step.glu_events.clear()
+    for _ in range(max(2, steps // 10)):
+        step.run(time_glu=True)
+    torch.cuda.synchronize()
+    glu_us = 1000 * sum(a.elapsed_time(b) for a, b in step.glu_events) / len(step.glu_events)
+    weight_bytes = LAYERS * LAYER_BYTES
+    gbs = weight_bytes / (ms * 1e-3) / 1e9
+    achieved = glu_bytes(B) / (glu_us * 1e-6) / 1e9
+    return {
+        "ms_per_step": ms,
+        "weight_gbs": gbs,
+        "hbm_frac": gbs / HBM_PEAK_GBS,
+        "tok_s": B * 1000.0 / ms,
+        "glu_us": glu_us,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": f"matvec_kernel<Q4_K,B={B},GLU> gate+up 2x14336x4096",
+                     "bytes_per_launch": glu_bytes(B)},  # fmt: skip
+    }
+
+
+def cpu_baseline(seconds=10.0, cap=30.0):
+    """leat's LEAT_KERNELS=ref product (f32 activations, dequantize in ggml's order, f32 sums),
+    restated in C with OpenMP, over one synthetic layer's 7 matrices at B=1, repeated for about
+    `seconds` (at most `cap`): weight GB/s, the median layer pass."""
+    import numpy as np
+
+    from oracle import leat_oracle as O
+
+    path = ROOT / "oracle" / "libleatref.so"
+    if not path.exists():
+        import subprocess
+
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    lib = ctypes.CDLL(str(path))
+    lib.leat_ref_linear.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]  # fmt: skip
+    rng = np.random.default_rng(0)
+    mats = [(t, r, c, O.matrix_blocks(t, r, c, rng)) for _, t, r, c in MATRICES]
+    x = {c: rng.standard_normal(c).astype(np.float32) for c in (HIDDEN, FFN)}
+    out = np.zeros(FFN, np.float32)
+    times, begin = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        for t, r, c, b in mats:
+            assert lib.leat_ref_linear(t, b.ctypes.data, r, c, x[c].ctypes.data, 1, out.ctypes.data) == 0
+        times.append(time.perf_counter() - t0)
+        elapsed = time.perf_counter() - begin
+        if (elapsed >= seconds and len(times) >= 5) or elapsed >= cap:
+            break
+    per_layer = sorted(times)[len(times) // 2]
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {
+        "value": LAYER_BYTES / per_layer / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"one Llama-3-8B layer's 7 matrices (q,k,v,o,gate,up Q4_K; down Q6_K; {LAYER_BYTES} B) "
+        f"at B=1, f32 activations, {len(times)} passes in {time.perf_counter() - begin:.1f} s, median",
+        "tok_s_equiv": 1.0 / (per_layer * LAYERS),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build's path runs on a single MI355X, and no "
+              "multi-GPU configuration is part of it (see the sharding design).", file=sys.stderr)  # fmt: skip
+        sys.exit(2)
+
+    import torch
+
+    from leat_amd import _lib
+
+    lib = _lib.lib()
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    layers = [
+        {name: synthetic_weights(torch, t, r, c, gen, device) for name, t, r, c in MATRICES}
+        for _ in range(LAYERS)
+    ]
+    torch.cuda.synchronize()
+    print(f"weights ready: {LAYERS} layers, {LAYERS * LAYER_BYTES / 1e9:.2f} GB", file=sys.stderr, flush=True)
+    b1 = measure(torch, lib, layers, 1, args.steps, args.warmup, device)
+    print(f"B=1: {b1['ms_per_step']:.3f} ms/step, {b1['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    b8 = measure(torch, lib, layers, 8, args.steps, args.warmup, device)
+    print(f"B=8: {b8['ms_per_step']:.3f} ms/step, {b8['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(b1["weight_gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(b1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "llama3-8b-q4_k_m decode linear layers (config 2 shapes, 32 layers)",
+                   "batch": 1, "layers": LAYERS, "weight_bytes_per_step": LAYERS * LAYER_BYTES,
+                   "seed": args.seed},  # fmt: skip
+        "hbm_frac": round(b1["hbm_frac"], 4),
+        "tok_s": round(b1["tok_s"], 1),
+        "b8": {"weight_gbs": round(b8["weight_gbs"], 1), "hbm_frac": round(b8["hbm_frac"], 4),
+               "tok_s": round(b8["tok_s"], 1), "ms_per_step": round(b8["ms_per_step"], 4),
+               "roofline": b8["roofline"]},  # fmt: skip
+        "roofline": b1["roofline"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

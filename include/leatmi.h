@@ -1,0 +1,85 @@
+/* leatmi: the C ABI of the MI355X (gfx950) kernels for leat's quantized-weight linear layers.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream (`stream`, a hipStream_t, or NULL
+ * for the null stream), allocates nothing, keeps no state between calls and does not synchronise.
+ * All pointers are device pointers the caller owns. Weights are GGUF blocks exactly as stored:
+ * a (rows, cols) matrix is rows * cols / elements blocks, row after row (leat/quant.py:234-251).
+ * Return value: 0, or -1 with a message in leat_last_error() (bad type, shape or pointer, or a
+ * failed launch). Reference paths below are in alkinun/leat.
+ */
+#ifndef LEATMI_H
+#define LEATMI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGMLType ids of the storage types these kernels read (leat/quant.py:14-46) */
+#define LEAT_Q8_0 8
+#define LEAT_Q4_K 12
+#define LEAT_Q6_K 14
+
+/* GLU kinds (leat/kernels/common.py:299-321) */
+#define LEAT_GLU_SILU 0
+#define LEAT_GLU_GELU 1
+#define LEAT_GLU_OAI 2
+
+/* The message of the last failed call on this thread. */
+const char *leat_last_error(void);
+/* ABI revision of this header, and the device architecture the kernels are built for. */
+int leat_abi_version(void);
+const char *leat_target(void);
+
+/* Replaces leat/kernels/quantize.py:92-109 quantize_q8(x, norm, rows). x (rows, n) f32, n a
+ * multiple of 32; norm_weight (n) f32 or NULL for no RMSNorm, eps its epsilon. Writes q
+ * (rows * n / 4) int32 words of four int8 values, d and s (rows * n / 32) f32: d = max|x|/127,
+ * q = roundf(x / d), s = d * sum(q) per group of 32. */
+int leat_quantize_q8(const float *x, int rows, int n, const float *norm_weight, float eps,
+                     int32_t *q, float *d, float *s, void *stream);
+
+/* Replaces the custom kernel of leat/kernels/matvec.py:362-380 matvecs() for one matrix
+ * (_matvec_kernel, :306-321): out[t * rows + r] = W[r] . x[t] (+ residual[t * rows + r] if
+ * residual is not NULL), x given as quantize_q8's (xq, xd, xs) for `tokens` rows of `cols`
+ * values. tokens: 1..8 or 16. cols: a multiple of 256 for Q4_K/Q6_K, of 64 for Q8_0. */
+int leat_matvec(int type, const void *w, int rows, int cols, const int32_t *xq, const float *xd,
+                const float *xs, int tokens, const float *residual, float *out, void *stream);
+
+/* Replaces the loop over ws of leat/kernels/matvec.py:372-380 (matvecs(x, *ws) sharing one
+ * quantization): `count` matrices of the same cols; consecutive ones of one type run in one
+ * launch (up to 4). outs[i] receives tokens * rows[i] values, token-major. */
+int leat_matvecs(int count, const int *types, const void *const *ws, const int *rows, int cols,
+                 const int32_t *xq, const float *xd, const float *xs, int tokens,
+                 float *const *outs, void *stream);
+
+/* Replaces leat/kernels/matvec.py:383-395 swiglu() (_swiglu_kernel, :324-337):
+ * out[t * rows + r] = glu(kind)(gate[r] . x[t], up[r] . x[t]), gate and up of one type and shape,
+ * both in one kernel. */
+int leat_glu_matvec(int type, const void *gate, const void *up, int rows, int cols,
+                    const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
+                    float *out, void *stream);
+
+/* Replaces the LEAT_KERNELS=ref linear layer, leat/ops.py:35-38 (x @ w.dequant().T with f32
+ * activations, not quantized): out[t * rows + r] = W[r] . x[t] (+ residual), W decoded in
+ * ggml's operation order, f32 sums. x (tokens, cols) f32; tokens 1..8 or 16. */
+int leat_matvec_f32x(int type, const void *w, int rows, int cols, const float *x, int tokens,
+                     const float *residual, float *out, void *stream);
+
+/* Replaces leat/quant.py:246-251 QTensor.dequant() for the types above: n_blocks blocks to
+ * n_blocks * elements f32, bit-identical to ggml's dequantize_row_* (no fused multiply-add). */
+int leat_dequantize(int type, const void *blocks, int64_t n_blocks, float *out, void *stream);
+
+/* Parity probe with no counterpart in leat (whose kernels keep these sums in registers,
+ * leat/kernels/matvec.py:114-181): the exact int32 sums of weight and activation integers per
+ * scale span, computed by the matvec kernels' own decode: groups of 32 for Q4_K (nibbles 0..15)
+ * and Q8_0, halves of 16 for Q6_K (q - 32). out[(t * rows + r) * spans + span], spans = cols/32
+ * (Q4_K, Q8_0) or cols/16 (Q6_K). */
+int leat_group_dots(int type, const void *w, int rows, int cols, const int32_t *xq, int tokens,
+                    int32_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEATMI_H */

@@ -1,0 +1,109 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels of the quantized-weight path.
+//
+// GGUF blocks are consumed exactly as stored (no repacking):
+//   Q8_0  34 B / 32 weights:  f16 d, int8 qs[32]                       (leat/quant.py:117-119)
+//   Q4_K 144 B / 256 weights: f16 d, f16 dmin, u8 scales[12], u8 qs[128] (leat/quant.py:190-197)
+//   Q6_K 210 B / 256 weights: u8 ql[128], u8 qh[64], i8 scales[16], f16 d (leat/quant.py:213-223)
+// Activations are q8 as leat's quantize_q8 writes them (leat/kernels/quantize.py:25-49): int8
+// values packed four per int32 word, per row, and f32 d and s = d * sum(q) per group of 32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace leat {
+
+enum GgmlType : int { Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+
+constexpr int WAVE = 64;
+constexpr int GROUP = 32;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// a 16-byte vector whose address is only known to be 4-byte aligned: global_load_dwordx4 needs
+// dword alignment only
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef u32x2 u32x2_a4 __attribute__((aligned(4)));
+
+__device__ __forceinline__ float f16_lo(uint32_t word) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(word & 0xFFFFu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t word) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(word >> 16));
+}
+
+// acc + the dot product of the four signed bytes of a and b (v_dot4_i32_i8)
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int acc) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, acc, false);
+}
+
+// 32 bits from byte `shift` (0..3) of the 64-bit (hi:lo)
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+// each byte b (< 2 * offset) of a word as the signed byte b - offset: b + 128 - offset stays in
+// its byte, and flipping the top bit makes it b - offset in two's complement
+__device__ __forceinline__ uint32_t minus_bytes(uint32_t q, uint32_t offset) {
+    return (q + (128u - offset) * 0x01010101u) ^ 0x80808080u;
+}
+
+// 16 bytes at a byte offset that is even but maybe not 4-aligned: 5 aligned dwords, realigned
+__device__ __forceinline__ void load16_even(const uint8_t* base, uint64_t off, uint32_t out[4]) {
+    const uint32_t* p = (const uint32_t*)(base + (off & ~(uint64_t)3));
+    uint32_t shift = (uint32_t)(off & 3);
+    u32x4 a = *(const u32x4_a4*)p;
+    uint32_t e = p[4];
+    out[0] = align_bytes(a[1], a[0], shift);
+    out[1] = align_bytes(a[2], a[1], shift);
+    out[2] = align_bytes(a[3], a[2], shift);
+    out[3] = align_bytes(e, a[3], shift);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));
+    return v;
+}
+
+// The GLU activations of leat/kernels/common.py:299-321: silu(g)*u, gelu(g)*u (tanh
+// approximation) and gpt-oss's clamped "oai" SwiGLU.
+enum GluKind : int { GLU_SILU = 0, GLU_GELU = 1, GLU_OAI = 2 };
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float glu(int kind, float g, float u) {
+    if (kind == GLU_OAI) {
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -7.0f), 7.0f);
+        return g * sigmoid(1.702f * g) * (u + 1.0f);
+    }
+    if (kind == GLU_GELU) {
+        const float c = 1.5957691216057308f;  // 2 * sqrt(2 / pi)
+        return g * sigmoid(c * (g + 0.044715f * g * g * g)) * u;
+    }
+    return g * sigmoid(g) * u;
+}
+
+}  // namespace leat
+
+// ---------------------------------------------------------------- host-side error plumbing
+namespace leat {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace leat
+
+#define LEAT_REQUIRE(cond, ...)          \
+    do {                                 \
+        if (!(cond)) {                   \
+            ::leat::set_error(__VA_ARGS__); \
+            return -1;                   \
+        }                                \
+    } while (0)

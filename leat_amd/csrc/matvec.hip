@@ -1,0 +1,222 @@
+// Decode-path matrix-vector products on GGUF blocks as stored: y[t, row] = W[row] . x[t] for up
+// to 16 tokens, every weight read once for all tokens (leat/kernels/matvec.py:1-4, 306-395).
+//
+// One wave64 owns R consecutive rows (of each of NM matrices: NM = 2 for gate and up). Its lanes
+// take the rows' tasks in turn (a task is 32 weights of Q4_K/Q6_K, 64 of Q8_0, so rows of 4096
+// and 14336 weights are whole turns), load each token's activation words once and use them for
+// all R rows, take int32 dot products with v_dot4_i32_i8 and combine them in f32 per scale span;
+// the wave then sums its lanes and lane 0 stores. Several matrices that share the activations
+// (q, k and v) run in one launch: waves are numbered across them.
+#include "blocks.h"
+
+namespace leat {
+
+constexpr int MAX_MATS = 4;
+
+struct MatvecArgs {
+    const uint8_t* w[MAX_MATS];
+    float* out[MAX_MATS];
+    int rows[MAX_MATS];
+    int wave_start[MAX_MATS + 1];  // first wave of each matrix; wave_start[count] = total
+    int count;
+    int cols;
+    const int32_t* xq;
+    const float* xd;
+    const float* xs;
+    const float* residual;  // MODE_RESIDUAL: tokens * rows[0]
+    int kind;               // MODE_GLU: the GLU kind; w[0] gate, w[1] up, out[0]
+};
+
+enum Mode : int { MODE_PLAIN = 0, MODE_RESIDUAL = 1, MODE_GLU = 2 };
+
+template <int TYPE, int B, int R, int MODE>
+__global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs args) {
+    using T = Task<TYPE>;
+    constexpr int NM = MODE == MODE_GLU ? 2 : 1;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
+    if (wave >= args.wave_start[args.count]) return;
+    int m = 0;
+    if (MODE != MODE_GLU) {
+        while (m + 1 < args.count && wave >= args.wave_start[m + 1]) m++;
+    }
+    const int rows = args.rows[m];
+    const int row0 = (wave - args.wave_start[m]) * R;
+    const int cols = args.cols, tasks = cols / T::TASK_W;
+
+    float acc[NM][R][B];
+#pragma unroll
+    for (int i = 0; i < NM; i++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int t = 0; t < B; t++) acc[i][r][t] = 0.0f;
+
+    for (int task = lane; task < tasks; task += WAVE) {
+        typename T::Raw raw[NM][R];
+#pragma unroll
+        for (int i = 0; i < NM; i++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = min(row0 + r, rows - 1);
+                raw[i][r] = T::load(MODE == MODE_GLU ? args.w[i] : args.w[m], row, cols, task);
+            }
+        ActQ act[B];
+#pragma unroll
+        for (int t = 0; t < B; t++) act[t] = load_act<TYPE>(args.xq, args.xd, args.xs, cols, t, task);
+#pragma unroll
+        for (int i = 0; i < NM; i++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const typename T::Dec dec = T::decode(raw[i][r], task);
+#pragma unroll
+                for (int t = 0; t < B; t++) acc[i][r][t] += T::combine(dec, act[t], T::dots(dec, act[t]));
+            }
+    }
+
+#pragma unroll
+    for (int i = 0; i < NM; i++)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int t = 0; t < B; t++) acc[i][r][t] = wave_sum(acc[i][r][t]);
+
+    if (lane == 0) {
+        float* out = args.out[MODE == MODE_GLU ? 0 : m];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = row0 + r;
+            if (row >= rows) break;
+#pragma unroll
+            for (int t = 0; t < B; t++) {
+                const int64_t at = (int64_t)t * rows + row;
+                float v = acc[0][r][t];
+                if (MODE == MODE_GLU) v = glu(args.kind, acc[0][r][t], acc[NM - 1][r][t]);
+                if (MODE == MODE_RESIDUAL) v += args.residual[at];
+                out[at] = v;
+            }
+        }
+    }
+}
+
+// rows per wave for B tokens: with more tokens the activation loads a wave shares across its
+// rows cost more than the weights' (the reference's _per_warp, leat/kernels/matvec.py:340-347)
+template <int B, int MODE>
+constexpr int rows_per_wave() {
+    return MODE == MODE_GLU ? 1 : (B <= 8 ? 2 : 1);
+}
+
+template <int TYPE, int B, int MODE>
+static int launch_b(MatvecArgs& a, hipStream_t stream) {
+    constexpr int R = rows_per_wave<B, MODE>();
+    int total = 0;
+    for (int i = 0; i < a.count; i++) {
+        a.wave_start[i] = total;
+        total += (a.rows[i] + R - 1) / R;
+    }
+    a.wave_start[a.count] = total;
+    const int blocks = (total + 3) / 4;
+    hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE>), dim3(blocks), dim3(256), 0, stream, a);
+    return check_launch("matvec");
+}
+
+template <int TYPE, int MODE>
+static int launch_t(MatvecArgs& a, int tokens, hipStream_t s) {
+    switch (tokens) {
+    case 1: return launch_b<TYPE, 1, MODE>(a, s);
+    case 2: return launch_b<TYPE, 2, MODE>(a, s);
+    case 3: return launch_b<TYPE, 3, MODE>(a, s);
+    case 4: return launch_b<TYPE, 4, MODE>(a, s);
+    case 5: return launch_b<TYPE, 5, MODE>(a, s);
+    case 6: return launch_b<TYPE, 6, MODE>(a, s);
+    case 7: return launch_b<TYPE, 7, MODE>(a, s);
+    case 8: return launch_b<TYPE, 8, MODE>(a, s);
+    case 16: return launch_b<TYPE, 16, MODE>(a, s);
+    default: set_error("matvec: %d tokens (1..8 or 16 supported)", tokens); return -1;
+    }
+}
+
+template <int MODE>
+static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
+    switch (type) {
+    case Q4_K: return launch_t<Q4_K, MODE>(a, tokens, s);
+    case Q6_K: return launch_t<Q6_K, MODE>(a, tokens, s);
+    case Q8_0: return launch_t<Q8_0, MODE>(a, tokens, s);
+    default: set_error("matvec: unsupported type %d", type); return -1;
+    }
+}
+
+int check_cols(int type, int cols) {
+    if (type == Q4_K || type == Q6_K) {
+        LEAT_REQUIRE(cols > 0 && cols % 256 == 0, "cols %d is not a whole number of 256-weight blocks", cols);
+    } else if (type == Q8_0) {
+        LEAT_REQUIRE(cols > 0 && cols % 64 == 0, "cols %d is not a whole number of Q8_0 block pairs", cols);
+    } else {
+        set_error("unsupported type %d", type);
+        return -1;
+    }
+    return 0;
+}
+
+}  // namespace leat
+
+using namespace leat;
+
+extern "C" int leat_matvecs(int count, const int* types, const void* const* ws, const int* rows, int cols,
+                            const int32_t* xq, const float* xd, const float* xs, int tokens,
+                            float* const* outs, void* stream) {
+    LEAT_REQUIRE(count >= 1, "matvecs: no matrices");
+    LEAT_REQUIRE(xq && xd && xs, "matvecs: null activations");
+    int done = 0;
+    while (done < count) {
+        // consecutive matrices of one type share a launch, up to MAX_MATS
+        MatvecArgs a = {};
+        const int type = types[done];
+        if (check_cols(type, cols)) return -1;
+        while (done < count && types[done] == type && a.count < MAX_MATS) {
+            LEAT_REQUIRE(ws[done] && outs[done] && rows[done] > 0, "matvecs: bad matrix %d", done);
+            a.w[a.count] = (const uint8_t*)ws[done];
+            a.out[a.count] = outs[done];
+            a.rows[a.count] = rows[done];
+            a.count++;
+            done++;
+        }
+        a.cols = cols;
+        a.xq = xq, a.xd = xd, a.xs = xs;
+        if (launch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream)) return -1;
+    }
+    return 0;
+}
+
+extern "C" int leat_matvec(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd,
+                           const float* xs, int tokens, const float* residual, float* out, void* stream) {
+    if (check_cols(type, cols)) return -1;
+    LEAT_REQUIRE(w && out && xq && xd && xs && rows > 0, "matvec: null pointer or empty matrix");
+    MatvecArgs a = {};
+    a.w[0] = (const uint8_t*)w;
+    a.out[0] = out;
+    a.rows[0] = rows;
+    a.count = 1;
+    a.cols = cols;
+    a.xq = xq, a.xd = xd, a.xs = xs;
+    a.residual = residual;
+    return residual ? launch<MODE_RESIDUAL>(type, a, tokens, (hipStream_t)stream)
+                    : launch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream);
+}
+
+extern "C" int leat_glu_matvec(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
+                               const float* xd, const float* xs, int tokens, int kind, float* out, void* stream) {
+    if (check_cols(type, cols)) return -1;
+    LEAT_REQUIRE(gate && up && out && xq && xd && xs && rows > 0, "glu_matvec: null pointer or empty matrix");
+    LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matvec: unknown GLU kind %d", kind);
+    MatvecArgs a = {};
+    a.w[0] = (const uint8_t*)gate;
+    a.w[1] = (const uint8_t*)up;
+    a.out[0] = out;
+    a.rows[0] = rows;
+    a.count = 1;
+    a.cols = cols;
+    a.xq = xq, a.xd = xd, a.xs = xs;
+    a.kind = kind;
+    return launch<MODE_GLU>(type, a, tokens, (hipStream_t)stream);
+}
