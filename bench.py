@@ -82,7 +82,6 @@ class Step:
         self.qkv = [torch.empty(B * r, **f32) for _, _, r, _ in MATRICES[:3]]
         self.h = torch.empty(B, HIDDEN, **f32)
         self.g = torch.empty(B, FFN, **f32)
-        self.glu_events = []
 
     def quantize(self, x, n, out, norm):
         q, d, s = out
@@ -93,7 +92,14 @@ class Step:
     def _stream(self):
         return self.torch.cuda.current_stream().cuda_stream
 
-    def run(self, time_glu=False):
+    def run_glu_only(self):
+        xq, xd, xs = self.q8[HIDDEN]
+        st = self._stream()
+        for w in self.layers:
+            _call(self.lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
+                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), self.B, 0, self.g.data_ptr(), st)  # fmt: skip
+
+    def run(self):
         torch, lib, B = self.torch, self.lib, self.B
         st = self._stream()
         for i, w in enumerate(self.layers):
@@ -112,14 +118,8 @@ class Step:
             _call(lib, "leat_matvec", Q4_K, w["o"].data_ptr(), HIDDEN, HIDDEN, aq.data_ptr(), ad.data_ptr(),
                   as_.data_ptr(), B, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
             self.quantize(self.h, HIDDEN, self.q8[HIDDEN], True)
-            if time_glu:
-                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                ev[0].record()
             _call(lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
                   xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), st)  # fmt: skip
-            if time_glu:
-                ev[1].record()
-                self.glu_events.append(ev)
             gq, gd, gs = self.q8[FFN]
             self.quantize(self.g, FFN, self.q8[FFN], False)
             _call(lib, "leat_matvec", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, gq.data_ptr(), gd.data_ptr(),
@@ -154,12 +154,20 @@ def measure(torch, lib, layers, B, steps, warmup, device):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    # the dominant kernel, timed by events around each of its launches (eager steps)
-    step.glu_events.clear()
-    for _ in range(max(2, steps // 10)):
-        step.run(time_glu=True)
+    # the dominant kernel alone: its 32 launches of a step (one per layer, distinct weights)
+    # back to back in a graph, timed by events on the stream they run on
+    glu_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(glu_graph):
+        step.run_glu_only()
+    glu_graph.replay()
     torch.cuda.synchronize()
-    glu_us = 1000 * sum(a.elapsed_time(b) for a, b in step.glu_events) / len(step.glu_events)
+    reps = max(3, steps // 5)
+    start.record()
+    for _ in range(reps):
+        glu_graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    glu_us = 1000 * start.elapsed_time(end) / (reps * LAYERS)
     weight_bytes = LAYERS * LAYER_BYTES
     gbs = weight_bytes / (ms * 1e-3) / 1e9
     achieved = glu_bytes(B) / (glu_us * 1e-6) / 1e9
@@ -171,7 +179,7 @@ def measure(torch, lib, layers, B, steps, warmup, device):
         "glu_us": glu_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": f"matvec_kernel<Q4_K,B={B},GLU> gate+up 2x14336x4096",
+                     "kernel": f"gate+up GLU matvec, Q4_K 2x14336x4096, B={B}",
                      "bytes_per_launch": glu_bytes(B)},  # fmt: skip
     }
 

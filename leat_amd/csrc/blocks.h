@@ -48,8 +48,8 @@ struct Task<Q4_K> {
         const int nb = cols / WEIGHTS, b = task >> 3, k = task & 7;
         const uint8_t* blk = w + ((int64_t)row * nb + b) * BYTES;
         Raw r;
-        r.hdr = *(const u32x4*)blk;
-        r.qs = *(const u32x4*)(blk + 16 + 16 * k);  // 32j + 16h = 16k
+        r.hdr = stream_load((const u32x4*)blk);
+        r.qs = stream_load((const u32x4*)(blk + 16 + 16 * k));  // 32j + 16h = 16k
         return r;
     }
     // get_scale_min_k4 for sub-blocks s and s+1 (s even), leat/quant.py:182-187
@@ -179,13 +179,13 @@ struct Task<Q8_0> {
         Raw r;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            u32x4 q = *(const u32x4_a4*)(p + 4 * i);
+            u32x4 q = stream_load((const u32x4_a4*)(p + 4 * i));
             r.v[4 * i] = q[0];
             r.v[4 * i + 1] = q[1];
             r.v[4 * i + 2] = q[2];
             r.v[4 * i + 3] = q[3];
         }
-        r.v[16] = p[16];
+        r.v[16] = stream_load(p + 16);
         return r;
     }
     __device__ static Dec decode(const Raw& r, int task) {
@@ -241,6 +241,34 @@ __device__ __forceinline__ ActQ load_act(const int32_t* xq, const float* xd, con
     a.d1 = dd[g1];
     if (TYPE == Q4_K) {
         const float* ss = xs + (int64_t)t * (cols / GROUP);
+        a.s0 = ss[g0];
+        a.s1 = ss[g1];
+    }
+    return a;
+}
+
+// the same from LDS, where a workgroup staged B tokens' activations: xq words (B * cols/4),
+// then d (B * cols/32), then s (B * cols/32)
+template <int TYPE>
+__device__ __forceinline__ ActQ load_act_lds(const uint32_t* lds, int tokens, int cols, int t, int task) {
+    using T = Task<TYPE>;
+    int g0, g1, word;
+    T::act_at(cols, task, &g0, &g1, &word);
+    const uint32_t* q = lds + t * (cols / 4);
+    const float* dd = (const float*)(lds + tokens * (cols / 4)) + t * (cols / GROUP);
+    const float* ss = dd + tokens * (cols / GROUP);
+    ActQ a;
+#pragma unroll
+    for (int i = 0; i < T::WORDS; i += 4) {
+        u32x4 v0 = *(const u32x4*)(q + g0 * 8 + word + i);
+        u32x4 v1 = *(const u32x4*)(q + g1 * 8 + word + i);
+        a.x0[i] = v0[0], a.x0[i + 1] = v0[1], a.x0[i + 2] = v0[2], a.x0[i + 3] = v0[3];
+        a.x1[i] = v1[0], a.x1[i + 1] = v1[1], a.x1[i + 2] = v1[2], a.x1[i + 3] = v1[3];
+    }
+    a.d0 = dd[g0];
+    a.d1 = dd[g1];
+    a.s0 = a.s1 = 0.0f;
+    if (TYPE == Q4_K) {
         a.s0 = ss[g0];
         a.s1 = ss[g1];
     }

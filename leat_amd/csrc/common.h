@@ -48,12 +48,26 @@ __device__ __forceinline__ uint32_t minus_bytes(uint32_t q, uint32_t offset) {
     return (q + (128u - offset) * 0x01010101u) ^ 0x80808080u;
 }
 
+// a weight load. Marking them nontemporal (streamed once) measured slower on gfx950: a block's
+// bytes straddle 128-byte lines that neighbouring loads read again, and the hint evicts them first.
+#ifndef LEAT_NONTEMPORAL
+#define LEAT_NONTEMPORAL 0
+#endif
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) {
+#if LEAT_NONTEMPORAL
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
 // 16 bytes at a byte offset that is even but maybe not 4-aligned: 5 aligned dwords, realigned
 __device__ __forceinline__ void load16_even(const uint8_t* base, uint64_t off, uint32_t out[4]) {
     const uint32_t* p = (const uint32_t*)(base + (off & ~(uint64_t)3));
     uint32_t shift = (uint32_t)(off & 3);
-    u32x4 a = *(const u32x4_a4*)p;
-    uint32_t e = p[4];
+    u32x4 a = stream_load((const u32x4_a4*)p);
+    uint32_t e = stream_load(p + 4);
     out[0] = align_bytes(a[1], a[0], shift);
     out[1] = align_bytes(a[2], a[1], shift);
     out[2] = align_bytes(a[3], a[2], shift);
@@ -65,6 +79,21 @@ __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
     return v;
+}
+
+// the sum over the wave's 64 lanes, in every lane, by DPP moves (quad permutes, row shifts and
+// row broadcasts): no LDS traffic, unlike a shuffle's ds_bpermute
+#define LEAT_DPP(v, ctrl, rm, bm) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rm, bm, false))
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += LEAT_DPP(v, 0xB1, 0xF, 0xF);   // quad_perm [1,0,3,2]
+    v += LEAT_DPP(v, 0x4E, 0xF, 0xF);   // quad_perm [2,3,0,1]: each lane holds its quad's sum
+    v += LEAT_DPP(v, 0x114, 0xF, 0xE);  // row_shr:4 into banks 1..3
+    v += LEAT_DPP(v, 0x118, 0xF, 0xC);  // row_shr:8 into banks 2..3: lane 15 of a row holds its sum
+    v += LEAT_DPP(v, 0x142, 0xA, 0xF);  // row_bcast:15 into rows 1 and 3
+    v += LEAT_DPP(v, 0x143, 0xC, 0xF);  // row_bcast:31 into rows 2 and 3: lane 63 holds the total
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {

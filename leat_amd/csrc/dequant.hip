@@ -151,6 +151,7 @@ __global__ void zero_kernel(int32_t* p, int64_t n) {
 }
 
 int check_cols(int type, int cols);
+int check_ptrs(int type, const void* w, const void* xq);
 
 }  // namespace leat
 
@@ -198,6 +199,7 @@ extern "C" int leat_matvec_f32x(int type, const void* w, int rows, int cols, con
                                 const float* residual, float* out, void* stream) {
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(w && x && out && rows > 0, "matvec_f32x: null pointer or empty matrix");
+    LEAT_REQUIRE((uintptr_t)x % 16 == 0, "matvec_f32x: activations must start 16-byte aligned");
     const uint8_t* b = (const uint8_t*)w;
     hipStream_t st = (hipStream_t)stream;
     switch (type) {
@@ -211,6 +213,7 @@ extern "C" int leat_group_dots(int type, const void* w, int rows, int cols, cons
                                int32_t* out, void* stream) {
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(w && xq && out && rows > 0 && tokens > 0, "group_dots: null pointer or empty input");
+    if (check_ptrs(type, w, xq)) return -1;
     hipStream_t st = (hipStream_t)stream;
     const uint8_t* b = (const uint8_t*)w;
     const int task_w = type == Q8_0 ? 64 : 32;

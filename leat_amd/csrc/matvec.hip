@@ -8,10 +8,11 @@
 // the wave then sums its lanes and lane 0 stores. Several matrices that share the activations
 // (q, k and v) run in one launch: waves are numbered across them.
 #include "blocks.h"
+#include "mmv.h"
 
 namespace leat {
 
-constexpr int MAX_MATS = 4;
+constexpr int MAX_MATS = MMV_MATS;
 
 struct MatvecArgs {
     const uint8_t* w[MAX_MATS];
@@ -29,10 +30,29 @@ struct MatvecArgs {
 
 enum Mode : int { MODE_PLAIN = 0, MODE_RESIDUAL = 1, MODE_GLU = 2 };
 
-template <int TYPE, int B, int R, int MODE>
+
+
+
+
+// U tasks of each row in flight per lane per iteration; LDS: the workgroup first stages the
+// tokens' activations in LDS (xq words, then d, then s) and the lanes read them there.
+template <int TYPE, int B, int R, int MODE, int U, bool LDS>
 __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs args) {
     using T = Task<TYPE>;
     constexpr int NM = MODE == MODE_GLU ? 2 : 1;
+    extern __shared__ uint32_t act_lds[];
+    const int cols = args.cols, tasks = cols / T::TASK_W;
+    if (LDS) {
+        const int words = B * (cols / 4), scales = B * (cols / GROUP);
+        const u32x4* q = (const u32x4*)args.xq;
+        for (int i = threadIdx.x; i < words / 4; i += blockDim.x) ((u32x4*)act_lds)[i] = q[i];
+        float* lds_d = (float*)(act_lds + words);
+        for (int i = threadIdx.x; i < scales; i += blockDim.x) {
+            lds_d[i] = args.xd[i];
+            if (TYPE == Q4_K) lds_d[scales + i] = args.xs[i];
+        }
+        __syncthreads();
+    }
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
     if (wave >= args.wave_start[args.count]) return;
@@ -42,7 +62,6 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs args) {
     }
     const int rows = args.rows[m];
     const int row0 = (wave - args.wave_start[m]) * R;
-    const int cols = args.cols, tasks = cols / T::TASK_W;
 
     float acc[NM][R][B];
 #pragma unroll
@@ -52,26 +71,38 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs args) {
 #pragma unroll
             for (int t = 0; t < B; t++) acc[i][r][t] = 0.0f;
 
-    for (int task = lane; task < tasks; task += WAVE) {
-        typename T::Raw raw[NM][R];
+    for (int first = lane; first < tasks; first += WAVE * U) {
+        typename T::Raw raw[U][NM][R];
 #pragma unroll
-        for (int i = 0; i < NM; i++)
+        for (int u = 0; u < U; u++) {
+            const int task = first + u * WAVE;
+            if (U > 1 && task >= tasks) break;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int row = min(row0 + r, rows - 1);
-                raw[i][r] = T::load(MODE == MODE_GLU ? args.w[i] : args.w[m], row, cols, task);
-            }
-        ActQ act[B];
+            for (int i = 0; i < NM; i++)
 #pragma unroll
-        for (int t = 0; t < B; t++) act[t] = load_act<TYPE>(args.xq, args.xd, args.xs, cols, t, task);
+                for (int r = 0; r < R; r++) {
+                    const int row = min(row0 + r, rows - 1);
+                    raw[u][i][r] = T::load(MODE == MODE_GLU ? args.w[i] : args.w[m], row, cols, task);
+                }
+        }
 #pragma unroll
-        for (int i = 0; i < NM; i++)
+        for (int u = 0; u < U; u++) {
+            const int task = first + u * WAVE;
+            if (U > 1 && task >= tasks) break;
+            ActQ act[B];
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const typename T::Dec dec = T::decode(raw[i][r], task);
+            for (int t = 0; t < B; t++)
+                act[t] = LDS ? load_act_lds<TYPE>(act_lds, B, cols, t, task)
+                             : load_act<TYPE>(args.xq, args.xd, args.xs, cols, t, task);
 #pragma unroll
-                for (int t = 0; t < B; t++) acc[i][r][t] += T::combine(dec, act[t], T::dots(dec, act[t]));
-            }
+            for (int i = 0; i < NM; i++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const typename T::Dec dec = T::decode(raw[u][i][r], task);
+#pragma unroll
+                    for (int t = 0; t < B; t++) acc[i][r][t] += T::combine(dec, act[t], T::dots(dec, act[t]));
+                }
+        }
     }
 
 #pragma unroll
@@ -106,6 +137,10 @@ constexpr int rows_per_wave() {
     return MODE == MODE_GLU ? 1 : (B <= 8 ? 2 : 1);
 }
 
+#ifndef LEAT_MATVEC_UNROLL
+#define LEAT_MATVEC_UNROLL 2
+#endif
+
 template <int TYPE, int B, int MODE>
 static int launch_b(MatvecArgs& a, hipStream_t stream) {
     constexpr int R = rows_per_wave<B, MODE>();
@@ -116,7 +151,15 @@ static int launch_b(MatvecArgs& a, hipStream_t stream) {
     }
     a.wave_start[a.count] = total;
     const int blocks = (total + 3) / 4;
-    hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE>), dim3(blocks), dim3(256), 0, stream, a);
+    // one or two tokens' activations fit LDS next to other workgroups on the CU; gate and up,
+    // two rows a wave, measured faster reading them from L2
+    const size_t lds = (size_t)B * (a.cols + a.cols / GROUP * 8);
+    if (MODE != MODE_GLU && B <= 2 && lds <= 40960) {
+        constexpr int U = B == 1 ? LEAT_MATVEC_UNROLL : 1;
+        hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE, U, true>), dim3(blocks), dim3(256), lds, stream, a);
+    } else {
+        hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE, 1, false>), dim3(blocks), dim3(256), 0, stream, a);
+    }
     return check_launch("matvec");
 }
 
@@ -144,6 +187,41 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     case Q8_0: return launch_t<Q8_0, MODE>(a, tokens, s);
     default: set_error("matvec: unsupported type %d", type); return -1;
     }
+}
+
+#ifndef LEAT_MMV_MIN_TOKENS
+#define LEAT_MMV_MIN_TOKENS 3  // the fewest tokens the matrix-core path takes
+#endif
+
+// the matrix-core path where it fits the shape, else the v_dot4 kernels
+template <int MODE>
+static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
+    const int nw = MODE == MODE_GLU ? 2 : a.count;
+    if (tokens >= LEAT_MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
+        MmvArgs m = {};
+        for (int i = 0; i < MAX_MATS; i++) {
+            m.w[i] = a.w[i];
+            m.out[i] = a.out[i];
+            m.rows[i] = a.rows[i];
+        }
+        m.count = a.count;
+        m.cols = a.cols;
+        m.tokens = tokens;
+        m.xq = a.xq, m.xd = a.xd, m.xs = a.xs;
+        m.residual = a.residual;
+        m.kind = a.kind;
+        return mmv_launch(type, MODE, m, s);
+    }
+    return launch<MODE>(type, a, tokens, s);
+}
+
+// Q4_K blocks are read as 16-byte vectors: their matrices start 16-byte aligned; Q6_K and Q8_0
+// blocks as aligned dwords from a 4-byte aligned start. Activation words are read 16 at a time.
+int check_ptrs(int type, const void* w, const void* xq) {
+    const uintptr_t need = type == Q4_K ? 16 : 4;
+    LEAT_REQUIRE((uintptr_t)w % need == 0, "weights of type %d must start %d-byte aligned", type, (int)need);
+    LEAT_REQUIRE(xq == nullptr || (uintptr_t)xq % 16 == 0, "activation words must start 16-byte aligned");
+    return 0;
 }
 
 int check_cols(int type, int cols) {
@@ -175,6 +253,7 @@ extern "C" int leat_matvecs(int count, const int* types, const void* const* ws, 
         if (check_cols(type, cols)) return -1;
         while (done < count && types[done] == type && a.count < MAX_MATS) {
             LEAT_REQUIRE(ws[done] && outs[done] && rows[done] > 0, "matvecs: bad matrix %d", done);
+            if (check_ptrs(type, ws[done], xq)) return -1;
             a.w[a.count] = (const uint8_t*)ws[done];
             a.out[a.count] = outs[done];
             a.rows[a.count] = rows[done];
@@ -183,7 +262,7 @@ extern "C" int leat_matvecs(int count, const int* types, const void* const* ws, 
         }
         a.cols = cols;
         a.xq = xq, a.xd = xd, a.xs = xs;
-        if (launch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream)) return -1;
+        if (dispatch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream)) return -1;
     }
     return 0;
 }
@@ -192,6 +271,7 @@ extern "C" int leat_matvec(int type, const void* w, int rows, int cols, const in
                            const float* xs, int tokens, const float* residual, float* out, void* stream) {
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(w && out && xq && xd && xs && rows > 0, "matvec: null pointer or empty matrix");
+    if (check_ptrs(type, w, xq)) return -1;
     MatvecArgs a = {};
     a.w[0] = (const uint8_t*)w;
     a.out[0] = out;
@@ -200,8 +280,8 @@ extern "C" int leat_matvec(int type, const void* w, int rows, int cols, const in
     a.cols = cols;
     a.xq = xq, a.xd = xd, a.xs = xs;
     a.residual = residual;
-    return residual ? launch<MODE_RESIDUAL>(type, a, tokens, (hipStream_t)stream)
-                    : launch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream);
+    return residual ? dispatch<MODE_RESIDUAL>(type, a, tokens, (hipStream_t)stream)
+                    : dispatch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream);
 }
 
 extern "C" int leat_glu_matvec(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
@@ -209,6 +289,7 @@ extern "C" int leat_glu_matvec(int type, const void* gate, const void* up, int r
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(gate && up && out && xq && xd && xs && rows > 0, "glu_matvec: null pointer or empty matrix");
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matvec: unknown GLU kind %d", kind);
+    if (check_ptrs(type, gate, xq) || check_ptrs(type, up, xq)) return -1;
     MatvecArgs a = {};
     a.w[0] = (const uint8_t*)gate;
     a.w[1] = (const uint8_t*)up;
@@ -218,5 +299,5 @@ extern "C" int leat_glu_matvec(int type, const void* gate, const void* up, int r
     a.cols = cols;
     a.xq = xq, a.xd = xd, a.xs = xs;
     a.kind = kind;
-    return launch<MODE_GLU>(type, a, tokens, (hipStream_t)stream);
+    return dispatch<MODE_GLU>(type, a, tokens, (hipStream_t)stream);
 }
