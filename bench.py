@@ -8,9 +8,9 @@ exactly as leat's decode step calls them (leat/model.py:497-558 via leat/ops.py:
 are 32 distinct layers of seeded synthetic blocks (4.41 GB, far beyond the 256 MB MALL), resident
 in HBM before the timed region; each step is one HIP-graph replay. `value` is weight bytes per
 step / step time, as leat's bench counts weight GB/s (leat/bench.py:71-82). The roofline object is
-for the dominant kernel (gate+up GLU matvec), timed with HIP events around each of its launches;
-the CPU baseline is the C restatement of leat's LEAT_KERNELS=ref product (oracle/leat_ref.c) on
-the host cores, over a bounded sample.
+for the dominant kernel (gate+up GLU matvec): a step's 32 launches of it back to back in a HIP
+graph, timed with HIP events on their stream; the CPU baseline is the C restatement of leat's
+LEAT_KERNELS=ref product (oracle/leat_ref.c) on the host cores, over a bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu]
 """

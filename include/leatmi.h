@@ -78,6 +78,21 @@ int leat_dequantize(int type, const void *blocks, int64_t n_blocks, float *out, 
 int leat_group_dots(int type, const void *w, int rows, int cols, const int32_t *xq, int tokens,
                     int32_t *out, void *stream);
 
+/* Replaces the custom kernel of leat/kernels/matmul.py:1051-1066 matmuls() (_matmul_kernel,
+ * :631-841, with its fixup :856-901) for many tokens: out[t * rows + r] = W[r] . x[t]
+ * (+ residual), x as quantize_q8's (xq, xd, xs) for `tokens` rows of `cols`. int8 products per
+ * group of 32 on matrix cores, scaled per group in f32. cols a multiple of 256 (512 for Q6_K);
+ * weights 4-byte and xq 16-byte aligned. */
+int leat_matmul(int type, const void *w, int rows, int cols, const int32_t *xq, const float *xd,
+                const float *xs, int tokens, const float *residual, float *out, void *stream);
+
+/* Replaces the gated product of leat/kernels/matmul.py:1069-1081 feed_forward() (_products with
+ * gated=True): out[t * rows + r] = glu(kind)(gate[r] . x[t], up[r] . x[t]), gate and up in one
+ * kernel. Same shape rules as leat_matmul. */
+int leat_glu_matmul(int type, const void *gate, const void *up, int rows, int cols,
+                    const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
+                    float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,8 @@ SIGNATURES: dict[str, list] = {
     "leat_matvec_f32x": [_i, _p, _i, _i, _p, _i, _p, _p, _p],
     "leat_dequantize": [_i, _p, _i64, _p, _p],
     "leat_group_dots": [_i, _p, _i, _i, _p, _i, _p, _p],
+    "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p],
+    "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p],
 }
 
 
