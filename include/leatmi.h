@@ -93,6 +93,34 @@ int leat_glu_matmul(int type, const void *gate, const void *up, int rows, int co
                     const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
                     float *out, void *stream);
 
+/* Replaces leat/kernels/experts.py:163-172 route() (_route_kernel, :132-160): for each of `tokens`
+ * rows of scores (tokens, experts) f32, the `used` best experts by repeated argmax (ties to the
+ * lower id; -inf and NaN count as the least finite score) as ids (tokens * used) int32, and the
+ * softmax of their scores as weights (tokens * used) f32. experts <= 256, used <= 64. */
+int leat_route(const float *scores, int tokens, int experts, int used, int32_t *ids, float *weights,
+               void *stream);
+
+/* Replaces the expert kernel of leat/kernels/experts.py:341-359 (_experts_swiglu_kernel,
+ * :209-238): out[p * rows + r] = glu(kind)(gate[e] row r . x[p / used] + gate_bias[e * rows + r],
+ * up[e] row r . x[p / used] + up_bias[e * rows + r]) for pairs p < pairs, e = ids[p], x as
+ * quantize_q8's (xq, xd, xs). gate and up: stacks of `experts` (rows, cols) matrices; up NULL:
+ * gate stacks both, each expert's gate rows before its up rows. Biases may be NULL. Each chosen
+ * expert's rows are read once for all the pairs routed to it. */
+int leat_experts_glu(int type, const void *gate, const void *up, int experts, int rows, int cols,
+                     const int32_t *xq, const float *xd, const float *xs, const int32_t *ids, int pairs,
+                     int used, const float *gate_bias, const float *up_bias, int kind, float *out,
+                     void *stream);
+
+/* Replaces the down kernel of leat/kernels/experts.py:360-371 (_experts_down_kernel, :241-270):
+ * out[t * rows + r] = sum over slots s < used of weights[p] * scales[e] * (w[e] row r . h[p]
+ * + bias[e * rows + r]) (+ residual[t * rows + r]), p = t * used + s, e = ids[p]; h the pairs'
+ * hidden states as quantize_q8's (hq, hd, hs), tokens * used rows of cols. w: a stack of
+ * `experts` (rows, cols) matrices. scales, bias and residual may be NULL. */
+int leat_experts_down(int type, const void *w, int experts, int rows, int cols, const int32_t *hq,
+                      const float *hd, const float *hs, const int32_t *ids, const float *weights,
+                      int tokens, int used, const float *scales, const float *bias,
+                      const float *residual, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,9 @@ SIGNATURES: dict[str, list] = {
     "leat_group_dots": [_i, _p, _i, _i, _p, _i, _p, _p],
     "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p],
     "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p],
+    "leat_route": [_p, _i, _i, _i, _p, _p, _p],
+    "leat_experts_glu": [_i, _p, _p, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p, _p],
+    "leat_experts_down": [_i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
 }
 
 
