@@ -12,7 +12,13 @@ for the dominant kernel (gate+up GLU matvec): a step's 32 launches of it back to
 graph, timed with HIP events on their stream; the CPU baseline is the C restatement of leat's
 LEAT_KERNELS=ref product (oracle/leat_ref.c) on the host cores, over a bounded sample.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu]
+Beside the headline line's decode figures it reports, as sub-objects, the other benchmark
+configurations: "prefill" (512 tokens through a layer's FFN on matrix cores, TOPS against the
+int8 MFMA peak) and "moe" (a Qwen3-30B-A3B-style mixture at B = 1 and 8, weight GB/s of the
+distinct chosen experts), each with the roofline of its dominant kernel.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu] [--legs prefill,moe]
+                    [--copy-probe]
 """
 
 from __future__ import annotations
@@ -184,6 +190,162 @@ def measure(torch, lib, layers, B, steps, warmup, device):
     }
 
 
+def _graph_us(torch, fn, reps, inner=1):
+    # fn's launches captured once in a HIP graph, replayed `reps` times back to back and timed by
+    # events on the stream they run on: microseconds per call of fn, `inner` calls per capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return 1000 * start.elapsed_time(end) / (reps * inner)
+
+
+PREFILL_TOKENS = 512
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def measure_prefill(torch, lib, w, reps, device):
+    """Config 4: 512 tokens x 4096 f32 N(0,1) through the FFN's products on the layer's Q4_K gate
+    and up (14336 x 4096) and Q6_K down (4096 x 14336), as leat's feed_forward runs them
+    (leat/kernels/matmul.py:1069-1081): norm+quantize, gate+up+GLU on matrix cores, quantize,
+    down (+residual). TOPS counts the int8 products' 2*T*rows*cols ops of the three matrices."""
+    T = PREFILL_TOKENS
+    f32 = dict(dtype=torch.float32, device=device)
+    i32 = dict(dtype=torch.int32, device=device)
+    gen = torch.Generator(device=device).manual_seed(4)
+    x = torch.randn(T, HIDDEN, generator=gen, **f32)
+    norm_w = torch.rand(HIDDEN, generator=gen, **f32) + 0.5
+    q8 = {n: (torch.empty(T * n // 4, **i32), torch.empty(T * n // 32, **f32), torch.empty(T * n // 32, **f32))
+          for n in (HIDDEN, FFN)}  # fmt: skip
+    hidden = torch.empty(T, FFN, **f32)
+    out = torch.empty(T, HIDDEN, **f32)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def quantize(src, n, norm):
+        q, d, s = q8[n]
+        wp, eps = (norm_w.data_ptr(), 1e-5) if norm else (None, 0.0)
+        _call(lib, "leat_quantize_q8", src.data_ptr(), T, n, wp, eps, q.data_ptr(), d.data_ptr(), s.data_ptr(), st())
+
+    def glu():
+        xq, xd, xs = q8[HIDDEN]
+        _call(lib, "leat_glu_matmul", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN, xq.data_ptr(),
+              xd.data_ptr(), xs.data_ptr(), T, 0, hidden.data_ptr(), st())  # fmt: skip
+
+    def down():
+        hq, hd, hs = q8[FFN]
+        _call(lib, "leat_matmul", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, hq.data_ptr(), hd.data_ptr(),
+              hs.data_ptr(), T, x.data_ptr(), out.data_ptr(), st())  # fmt: skip
+
+    def ffn():
+        quantize(x, HIDDEN, True)
+        glu()
+        quantize(hidden, FFN, False)
+        down()
+
+    ffn()
+    torch.cuda.synchronize()
+    ffn_us = _graph_us(torch, ffn, reps)
+    glu_us = _graph_us(torch, glu, reps)
+    down_us = _graph_us(torch, down, reps)
+    glu_ops, down_ops = 2 * T * 2 * FFN * HIDDEN, 2 * T * HIDDEN * FFN
+    tops = (glu_ops + down_ops) / (ffn_us * 1e-6) / 1e12
+    glu_tops = glu_ops / (glu_us * 1e-6) / 1e12
+    return {
+        "workload": "512 tokens x 4096: Q4_K gate+up 2x14336x4096 (GLU fused), Q6_K down 4096x14336 (+residual)",
+        "ffn_us": round(ffn_us, 1), "glu_us": round(glu_us, 1), "down_us": round(down_us, 1),
+        "tops": round(tops, 1), "int8_frac": round(tops / INT8_PEAK_TOPS, 4),
+        "down_tops": round(down_ops / (down_us * 1e-6) / 1e12, 1),
+        "roofline": {"bound": "mfma", "achieved": glu_tops, "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": glu_tops / INT8_PEAK_TOPS, "traffic": None,
+                     "kernel": "gate+up GLU matmul (MMQ), Q4_K 2x14336x4096, 512 tokens", "ops_per_launch": glu_ops},
+    }  # fmt: skip
+
+
+# config 5: a Qwen3-30B-A3B-style mixture layer, over as many layers as that model has, so a
+# step's chosen experts (24.5 MB a layer at B=1) far exceed the 256 MB MALL
+MOE_EXPERTS, MOE_USED, MOE_DIM, MOE_HIDDEN, MOE_LAYERS = 128, 8, 2048, 768, 48
+EXPERT_BYTES = 2 * nbytes(Q4_K, MOE_HIDDEN, MOE_DIM) + nbytes(Q6_K, MOE_DIM, MOE_HIDDEN)  # 3,059,712
+
+
+def measure_moe(torch, lib, B, steps, device, layers):
+    """Config 5: the mixture of one token (B=1) or 8 streams (B=8) through 48 layers of 128
+    experts (gate and up 768 x 2048 Q4_K, down 2048 x 768 Q6_K, top 8, router logits N(0,1)):
+    per layer route, norm+quantize, the chosen experts' gate+up+GLU, quantize, their down
+    (+residual), as leat's mixture on the matrix-vector kernels (leat/kernels/experts.py:
+    341-377). Weight bytes are each layer's distinct chosen experts, read once each."""
+    f32 = dict(dtype=torch.float32, device=device)
+    i32 = dict(dtype=torch.int32, device=device)
+    gen = torch.Generator(device=device).manual_seed(5)
+    P = B * MOE_USED
+    scores = [torch.randn(B, MOE_EXPERTS, generator=gen, **f32) for _ in range(MOE_LAYERS)]
+    xs = [torch.randn(B, MOE_DIM, generator=gen, **f32) for _ in range(2)]
+    norm_w = torch.rand(MOE_DIM, generator=gen, **f32) + 0.5
+    ids, weights = torch.empty(P, **i32), torch.empty(P, **f32)
+    xq, xd, xs_ = torch.empty(B * MOE_DIM // 4, **i32), torch.empty(B * MOE_DIM // 32, **f32), torch.empty(B * MOE_DIM // 32, **f32)
+    h = torch.empty(P, MOE_HIDDEN, **f32)
+    hq, hd, hs = torch.empty(P * MOE_HIDDEN // 4, **i32), torch.empty(P * MOE_HIDDEN // 32, **f32), torch.empty(P * MOE_HIDDEN // 32, **f32)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    distinct = []
+
+    def layer(i, w, which="all"):
+        x, x_next = xs[i % 2], xs[(i + 1) % 2]
+        if which in ("all",):
+            _call(lib, "leat_route", scores[i].data_ptr(), B, MOE_EXPERTS, MOE_USED, ids.data_ptr(), weights.data_ptr(), st())
+            _call(lib, "leat_quantize_q8", x.data_ptr(), B, MOE_DIM, norm_w.data_ptr(), 1e-5, xq.data_ptr(),
+                  xd.data_ptr(), xs_.data_ptr(), st())  # fmt: skip
+        if which in ("all", "glu"):
+            _call(lib, "leat_experts_glu", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), MOE_EXPERTS, MOE_HIDDEN,
+                  MOE_DIM, xq.data_ptr(), xd.data_ptr(), xs_.data_ptr(), ids.data_ptr(), P, MOE_USED, None, None, 0,
+                  h.data_ptr(), st())  # fmt: skip
+        if which in ("all",):
+            _call(lib, "leat_quantize_q8", h.data_ptr(), P, MOE_HIDDEN, None, 0.0, hq.data_ptr(), hd.data_ptr(),
+                  hs.data_ptr(), st())  # fmt: skip
+        if which in ("all", "down"):
+            _call(lib, "leat_experts_down", Q6_K, w["down"].data_ptr(), MOE_EXPERTS, MOE_DIM, MOE_HIDDEN,
+                  hq.data_ptr(), hd.data_ptr(), hs.data_ptr(), ids.data_ptr(), weights.data_ptr(), B, MOE_USED,
+                  None, None, x.data_ptr(), x_next.data_ptr(), st())  # fmt: skip
+
+    for i, w in enumerate(layers):  # eager once: checks every launch, and counts distinct experts
+        layer(i, w)
+        torch.cuda.synchronize()
+        distinct.append(len(set(ids.cpu().tolist())))
+    step_us = _graph_us(torch, lambda: [layer(i, w) for i, w in enumerate(layers)], steps)
+    # the two expert kernels alone, on the last layer's routing, over every layer's weights
+    glu_us = _graph_us(torch, lambda: [layer(i, w, "glu") for i, w in enumerate(layers)], steps) / MOE_LAYERS
+    down_us = _graph_us(torch, lambda: [layer(i, w, "down") for i, w in enumerate(layers)], steps) / MOE_LAYERS
+    last = distinct[-1]
+    step_bytes = sum(distinct) * EXPERT_BYTES
+    glu_bytes = last * 2 * nbytes(Q4_K, MOE_HIDDEN, MOE_DIM) + B * (MOE_DIM + MOE_DIM // 32 * 8) + P * MOE_HIDDEN * 4
+    gbs = step_bytes / (step_us * 1e-6) / 1e9
+    glu_gbs = glu_bytes / (glu_us * 1e-6) / 1e9
+    return {
+        "batch": B, "layers": MOE_LAYERS, "distinct_experts_per_layer": round(sum(distinct) / len(distinct), 2),
+        "us_per_layer": round(step_us / MOE_LAYERS, 2), "weight_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tok_s": round(B * 1e6 / step_us, 1),
+        "glu_us": round(glu_us, 2), "down_us": round(down_us, 2),
+        "roofline": {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": glu_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": f"expert gate+up GLU matvec, {last} of 128 experts 2x768x2048 Q4_K, B={B}",
+                     "bytes_per_launch": glu_bytes},
+    }  # fmt: skip
+
+
+def moe_layers(torch, device, seed):
+    gen = torch.Generator(device=device).manual_seed(seed + 100)
+    return [{"gate": synthetic_weights(torch, Q4_K, MOE_EXPERTS * MOE_HIDDEN, MOE_DIM, gen, device),
+             "up": synthetic_weights(torch, Q4_K, MOE_EXPERTS * MOE_HIDDEN, MOE_DIM, gen, device),
+             "down": synthetic_weights(torch, Q6_K, MOE_EXPERTS * MOE_DIM, MOE_HIDDEN, gen, device)}
+            for _ in range(MOE_LAYERS)]  # fmt: skip
+
+
 def cpu_baseline(seconds=10.0, cap=30.0):
     """leat's LEAT_KERNELS=ref product (f32 activations, dequantize in ggml's order, f32 sums),
     restated in C with OpenMP, over one synthetic layer's 7 matrices at B=1, repeated for about
@@ -233,6 +395,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--legs", default="prefill,moe", help="configurations beside decode: prefill, moe")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also copy 256 MiB device to device: the calibration kernel of HBM byte counters")  # fmt: skip
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's path runs on a single MI355X, and no "
@@ -256,6 +421,25 @@ def main():
     print(f"B=1: {b1['ms_per_step']:.3f} ms/step, {b1['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     b8 = measure(torch, lib, layers, 8, args.steps, args.warmup, device)
     print(f"B=8: {b8['ms_per_step']:.3f} ms/step, {b8['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    prefill = moe = None
+    if "prefill" in args.legs:
+        prefill = measure_prefill(torch, lib, layers[0], max(5, args.steps // 5), device)
+        print(f"prefill: FFN {prefill['ffn_us']:.0f} us, {prefill['tops']:.0f} TOPS", file=sys.stderr, flush=True)
+    del layers
+    torch.cuda.empty_cache()
+    if "moe" in args.legs:
+        experts = moe_layers(torch, device, args.seed)
+        moe = {f"b{B}": measure_moe(torch, lib, B, max(5, args.steps // 5), device, experts) for B in (1, 8)}
+        print(f"moe: B=1 {moe['b1']['us_per_layer']:.1f} us/layer, B=8 {moe['b8']['us_per_layer']:.1f} us/layer",
+              file=sys.stderr, flush=True)  # fmt: skip
+        del experts
+    if args.copy_probe:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
@@ -279,6 +463,8 @@ def main():
                "tok_s": round(b8["tok_s"], 1), "ms_per_step": round(b8["ms_per_step"], 4),
                "roofline": b8["roofline"]},  # fmt: skip
         "roofline": b1["roofline"],
+        "prefill": prefill,
+        "moe": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -85,10 +85,11 @@ __device__ __forceinline__ void stage_load(Stage<TYPE>& st, const uint8_t* w, in
         const int c = lane + 64 * i;
         if (c < Stage<TYPE>::CHUNKS) {
             const int r = c / G::CPR, part = c % G::CPR;
-            const int64_t row = min(row0 + r, rows - 1);
+            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
             // chunks past the row's end (the last stage's spare ones) repeat its last chunk
-            const int64_t off = min(s0 + 16 * part, row_bytes - 16);
-            st.v[i] = stream_load((const u32x4*)(w + row * row_bytes + off));
+            const uint32_t off = (uint32_t)min(s0 + 16 * part, row_bytes - 16);
+            // a 32-bit offset from the matrix's (uniform) start: matrices are under 4 GiB
+            st.v[i] = stream_load((const u32x4*)(w + (row * (uint32_t)row_bytes + off)));
         }
     }
 }
@@ -122,16 +123,19 @@ struct Acts {
     int cols;
     int s_off;   // the s table's offset in mmv_lds, in floats (after d's G * TP)
     int xq_off;  // the words' offset in mmv_lds, in words
-    // lane (token t, half h)'s 16 values of group g, zero for tokens past the last
-    __device__ v4i operand(int t, int h, int g, bool live) const {
-        v4i v = {};
-        if (live) {
-            if (XQ)
-                v = *(const v4i*)(mmv_lds + xq_off + t * (cols / 4) + g * 8 + 4 * h);
-            else
-                v = *(const v4i*)(q + (int64_t)t * (cols / 4) + g * 8 + 4 * h);
-        }
-        return v;
+    // the lane's (token t, half h) words: group g's 16 values are 8 g words on, in global memory
+    // (lq) or in LDS (lx); set once, so a group's address is a 32-bit offset from them
+    const uint32_t* lq;
+    uint32_t lx;
+    __device__ void at_lane(int t, int h) {
+        lq = q + (int64_t)t * (cols / 4) + 4 * h;
+        lx = (uint32_t)(xq_off + t * (cols / 4) + 4 * h);
+    }
+    // the lane's 16 values of group g. A lane past the last token reads token 0's: its results
+    // (rows of tokens that are not there) are never stored, so no branch is needed here
+    __device__ v4i operand(int g) const {
+        if (XQ) return *(const v4i*)(mmv_lds + lx + g * 8);
+        return *(const v4i*)(lq + g * 8);
     }
     // the scales of group g for the lane's result registers v = 0..NV-1
     __device__ void scales(int off, int g, int h, float (&out)[NV]) const {
@@ -158,7 +162,7 @@ template <int TYPE> struct Compute;
 template <>
 struct Compute<Q4_K> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, bool live, float (&acc)[NV]) {
+    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
         const uint32_t at = base + r * Geo<Q4_K>::RS;  // the block starts the chunk run
         const u32x4 hdr = lds16(at);
         const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
@@ -176,7 +180,7 @@ struct Compute<Q4_K> {
                 const uint32_t scv = s < 4 ? (x0 & 63u) : ((x2 & 15u) | ((x0 >> 2) & 0x30u));
                 const uint32_t mv = s < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
                 const float sc = d * (float)scv, mn = dmin * (float)mv;
-                const v16i D = mfma_i8(a.operand(r, h, g, live), e ? hi : lo);
+                const v16i D = mfma_i8(a.operand(g), e ? hi : lo);
                 float xd[NV], xs[NV];
                 a.scales(0, g, h, xd);
                 a.scales(a.s_off, g, h, xs);
@@ -192,11 +196,19 @@ struct Compute<Q4_K> {
 template <>
 struct Compute<Q6_K> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, bool live, float (&acc)[NV]) {
+    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
+        // odd blocks as a compile-time case: a run-time flag keeps both forms of every read live
+        if (b & 1)
+            run_<NV, true>(base, b, a, r, h, acc);
+        else
+            run_<NV, false>(base, b, a, r, h, acc);
+    }
+    template <int NV, bool ODD, class A>
+    __device__ static void run_(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
         // the block starts (210 b) mod 16 bytes into the row's chunk run: 2 bytes off a 4-byte
         // boundary for odd b
         const uint32_t at = base + r * Geo<Q6_K>::RS + ((210u * (uint32_t)b) & 15u);
-        const bool odd = (b & 1) != 0;
+        constexpr bool odd = ODD;
         const u32x4 scales = lds16_even(at + 192, odd);
         const uint32_t dword = lds4((at + 208) & ~3u);
         const float d = odd ? f16_hi(dword) : f16_lo(dword);
@@ -217,7 +229,7 @@ struct Compute<Q6_K> {
                         const uint32_t high = (qh[i] >> (2 * k)) & 0x03030303u;
                         q[i] = minus_bytes(low | (high << 4), 32);
                     }
-                    const v4i x = a.operand(r, h, g, live);
+                    const v4i x = a.operand(g);
                     const u32x4 zero = {};
                     const v16i D0 = mfma_i8(x, h == 0 ? q : zero);  // values 0..15 of the row
                     const v16i D1 = mfma_i8(x, h == 1 ? q : zero);  // values 16..31
@@ -238,7 +250,7 @@ struct Compute<Q6_K> {
 template <>
 struct Compute<Q8_0> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, bool live, float (&acc)[NV]) {
+    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
         // a stage is blocks b and b + 1 (68 bytes from a 4-byte aligned start, b even)
         const uint32_t at = base + r * Geo<Q8_0>::RS + ((34u * (uint32_t)b) & 15u);
 #pragma unroll
@@ -247,7 +259,7 @@ struct Compute<Q8_0> {
             const uint32_t dword = lds4(blk & ~3u);
             const float d = e ? f16_hi(dword) : f16_lo(dword);
             const u32x4 qs = lds16_even(blk + 2 + 16 * h, e == 0);
-            const v16i D = mfma_i8(a.operand(r, h, b + e, live), qs);
+            const v16i D = mfma_i8(a.operand(b + e), qs);
             float xd[NV];
             a.scales(0, b + e, h, xd);
 #pragma unroll
@@ -260,8 +272,11 @@ struct Compute<Q8_0> {
 // waves per SIMD the register budget allows: 4 (128 registers) for one Q4_K or Q8_0 matrix and
 // up to two tokens' results, 3 (168) for Q6_K's wider stages, else 2 (256). A wave keeps a stage
 // of its tile in flight, so a few waves per SIMD cover HBM's latency.
+#ifndef LEAT_MMV_GLU_OCC
+#define LEAT_MMV_GLU_OCC 2
+#endif
 constexpr int mmv_occupancy(int type, int mode, int nv) {
-    return mode == MMV_GLU || nv > 2 ? 2 : type == Q6_K ? 3 : 4;
+    return mode == MMV_GLU && nv > 2 ? LEAT_MMV_GLU_OCC : mode == MMV_GLU || nv > 2 ? 2 : type == Q6_K ? 3 : 4;
 }
 
 template <int TYPE>
@@ -327,7 +342,7 @@ void mmv_kernel(MmvArgs args) {
         __syncthreads();
     }
     const uint32_t regions = (uint32_t)table_bytes<TYPE, NV>(cols) + (XQ ? (uint32_t)tokens * cols : 0u);
-    const bool live = r < tokens;
+    acts.at_lane(r < tokens ? r : 0, h);
 
     float acc[NM][NV];
 #pragma unroll
@@ -348,8 +363,7 @@ void mmv_kernel(MmvArgs args) {
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int i = 0; i < NM; i++)
-            Compute<TYPE>::template run<NV>(regions + (wave * NM + i) * 32 * G::RS, k * G::BPS, acts, r, h, live,
-                                            acc[i]);
+            Compute<TYPE>::template run<NV>(regions + (wave * NM + i) * 32 * G::RS, k * G::BPS, acts, r, h, acc[i]);
     }
 
     // the S waves' sums of the tile, through LDS
@@ -414,7 +428,8 @@ static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
     const int stages = a.cols / weights_per_block<TYPE>() / Geo<TYPE>::BPS;
     // waves per tile: enough for the launch to fill the GPU, at most one per stage of a row
     const int want = (LEAT_MMV_WAVES + tiles - 1) / tiles;
-    if (want >= 8 && stages >= 8) return mmv_launch_s<TYPE, MODE, NV, 8>(a, st);
+    if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1)
+        if (want >= 8 && stages >= 8) return mmv_launch_s<TYPE, MODE, NV, 8>(a, st);
     if (want >= 4 && stages >= 4) return mmv_launch_s<TYPE, MODE, NV, 4>(a, st);
     return mmv_launch_s<TYPE, MODE, NV, 1>(a, st);
 }
