@@ -88,6 +88,8 @@ class Step:
         self.qkv = [torch.empty(B * r, **f32) for _, _, r, _ in MATRICES[:3]]
         self.h = torch.empty(B, HIDDEN, **f32)
         self.g = torch.empty(B, FFN, **f32)
+        # one or two tokens: the kernels quantize their own input, and the GLU its output
+        self.self_quantized = tokens <= 2
 
     def quantize(self, x, n, out, norm):
         q, d, s = out
@@ -98,36 +100,54 @@ class Step:
     def _stream(self):
         return self.torch.cuda.current_stream().cuda_stream
 
-    def run_glu_only(self):
-        xq, xd, xs = self.q8[HIDDEN]
-        st = self._stream()
-        for w in self.layers:
+    def glu(self, w):
+        # the layer's gate+up GLU launch, as run() issues it
+        B, st = self.B, self._stream()
+        gq, gd, gs = self.q8[FFN]
+        if self.self_quantized:
+            _call(self.lib, "leat_glu_matvec_f32", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
+                  self.h.data_ptr(), B, self.norm_w.data_ptr(), 1e-5, 0, None, gq.data_ptr(), gd.data_ptr(),
+                  gs.data_ptr(), st)  # fmt: skip
+        else:
+            xq, xd, xs = self.q8[HIDDEN]
             _call(self.lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
-                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), self.B, 0, self.g.data_ptr(), st)  # fmt: skip
+                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), st)  # fmt: skip
+
+    def run_glu_only(self):
+        for w in self.layers:
+            self.glu(w)
 
     def run(self):
-        torch, lib, B = self.torch, self.lib, self.B
+        lib, B = self.lib, self.B
         st = self._stream()
+        types = (ctypes.c_int * 3)(Q4_K, Q4_K, Q4_K)
+        rows = (ctypes.c_int * 3)(HIDDEN, KV, KV)
+        outs = (ctypes.c_void_p * 3)(*[o.data_ptr() for o in self.qkv])
+        xq, xd, xs = self.q8[HIDDEN]
+        aq, ad, as_ = self.q8b
+        gq, gd, gs = self.q8[FFN]
         for i, w in enumerate(self.layers):
             x, x_next = self.x[i % 2], self.x[(i + 1) % 2]
-            xq, xd, xs = self.q8[HIDDEN]
-            self.quantize(x, HIDDEN, self.q8[HIDDEN], True)
-            types = (ctypes.c_int * 3)(Q4_K, Q4_K, Q4_K)
             ptrs = (ctypes.c_void_p * 3)(*[w[n].data_ptr() for n in ("q", "k", "v")])
-            rows = (ctypes.c_int * 3)(HIDDEN, KV, KV)
-            outs = (ctypes.c_void_p * 3)(*[o.data_ptr() for o in self.qkv])
-            _call(lib, "leat_matvecs", 3, types, ptrs, rows, HIDDEN, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
-                  B, outs, st)  # fmt: skip
-            # the attention output stands in with q's product: same shape, realistic values
-            aq, ad, as_ = self.q8b
-            self.quantize(self.qkv[0], HIDDEN, self.q8b, False)
-            _call(lib, "leat_matvec", Q4_K, w["o"].data_ptr(), HIDDEN, HIDDEN, aq.data_ptr(), ad.data_ptr(),
-                  as_.data_ptr(), B, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
-            self.quantize(self.h, HIDDEN, self.q8[HIDDEN], True)
-            _call(lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
-                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), st)  # fmt: skip
-            gq, gd, gs = self.q8[FFN]
-            self.quantize(self.g, FFN, self.q8[FFN], False)
+            # norm + quantize + q, k, v; the attention output stands in with q's product (same
+            # shape, realistic values); quantize + o + residual; norm + quantize + gate, up, GLU;
+            # quantize + down + residual
+            if self.self_quantized:
+                _call(lib, "leat_matvecs_f32", 3, types, ptrs, rows, HIDDEN, x.data_ptr(), B,
+                      self.norm_w.data_ptr(), 1e-5, outs, st)  # fmt: skip
+                _call(lib, "leat_matvec_f32", Q4_K, w["o"].data_ptr(), HIDDEN, HIDDEN, self.qkv[0].data_ptr(), B,
+                      None, 0.0, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
+                self.glu(w)
+            else:
+                self.quantize(x, HIDDEN, self.q8[HIDDEN], True)
+                _call(lib, "leat_matvecs", 3, types, ptrs, rows, HIDDEN, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
+                      B, outs, st)  # fmt: skip
+                self.quantize(self.qkv[0], HIDDEN, self.q8b, False)
+                _call(lib, "leat_matvec", Q4_K, w["o"].data_ptr(), HIDDEN, HIDDEN, aq.data_ptr(), ad.data_ptr(),
+                      as_.data_ptr(), B, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
+                self.quantize(self.h, HIDDEN, self.q8[HIDDEN], True)
+                self.glu(w)
+                self.quantize(self.g, FFN, self.q8[FFN], False)
             _call(lib, "leat_matvec", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, gq.data_ptr(), gd.data_ptr(),
                   gs.data_ptr(), B, self.h.data_ptr(), x_next.data_ptr(), st)  # fmt: skip
 
@@ -138,9 +158,13 @@ def _call(lib, name, *args):
 
 
 def glu_bytes(B):
-    # algorithmic bytes of one gate+up GLU launch: both matrices, q8 activations (int8 + d + s),
-    # f32 outputs
-    return 2 * nbytes(Q4_K, FFN, HIDDEN) + B * (HIDDEN + HIDDEN // 32 * 8) + B * FFN * 4
+    # algorithmic bytes of one gate+up GLU launch: both matrices, then for one or two tokens the
+    # f32 input read (and quantized in the kernel) and the q8 output written (int8 + d + s); for
+    # more tokens q8 input and f32 output
+    weights = 2 * nbytes(Q4_K, FFN, HIDDEN)
+    if B <= 2:
+        return weights + B * HIDDEN * 4 + B * (FFN + FFN // 32 * 8)
+    return weights + B * (HIDDEN + HIDDEN // 32 * 8) + B * FFN * 4
 
 
 def measure(torch, lib, layers, B, steps, warmup, device):
@@ -185,7 +209,8 @@ def measure(torch, lib, layers, B, steps, warmup, device):
         "glu_us": glu_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": f"gate+up GLU matvec, Q4_K 2x14336x4096, B={B}",
+                     "kernel": f"gate+up GLU matvec, Q4_K 2x14336x4096, B={B}"
+                               + (" (quantizes its f32 input and its output)" if B <= 2 else ""),
                      "bytes_per_launch": glu_bytes(B)},  # fmt: skip
     }
 

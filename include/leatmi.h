@@ -60,6 +60,32 @@ int leat_glu_matvec(int type, const void *gate, const void *up, int rows, int co
                     const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
                     float *out, void *stream);
 
+/* Replaces the whole of leat/kernels/matvec.py:362-380 matvecs(x, *ws, norm) for one or two
+ * tokens: quantize_q8 of x (after RMSNorm with norm_weight and eps when norm_weight is not NULL)
+ * and the products, in one launch. Each workgroup quantizes x itself with leat_quantize_q8's
+ * arithmetic, so the outputs are bit-identical to leat_quantize_q8 followed by leat_matvecs.
+ * x (tokens, cols) f32, 16-byte aligned; 1 to 4 matrices of one type, Q4_K (cols a multiple of
+ * 256, at most 8192) or Q8_0 (a multiple of 64, at most 8192); tokens 1 or 2. */
+int leat_matvecs_f32(int count, const int *types, const void *const *ws, const int *rows, int cols,
+                     const float *x, int tokens, const float *norm_weight, float eps,
+                     float *const *outs, void *stream);
+
+/* The same for one matrix with an optional residual (leat/kernels/matvec.py:362-380 with
+ * residual): out[t * rows + r] = W[r] . q8(x[t]) (+ residual[t * rows + r]). */
+int leat_matvec_f32(int type, const void *w, int rows, int cols, const float *x, int tokens,
+                    const float *norm_weight, float eps, const float *residual, float *out,
+                    void *stream);
+
+/* Replaces leat/kernels/matvec.py:383-395 swiglu(x, gate, up, norm, kind) for one or two tokens
+ * in one launch, x quantized inside as in leat_matvecs_f32. out (tokens * rows f32) may be NULL
+ * when hq is given. When hq, hd and hs are given (rows a multiple of 32) the kernel also writes
+ * leat_quantize_q8 of its outputs, (tokens, rows) as (tokens * rows / 4) words and
+ * (tokens * rows / 32) scales and sums: the down product's input, as leat's feed_forward
+ * quantizes it (leat/ops.py:41-55), without another launch. */
+int leat_glu_matvec_f32(int type, const void *gate, const void *up, int rows, int cols,
+                        const float *x, int tokens, const float *norm_weight, float eps, int kind,
+                        float *out, int32_t *hq, float *hd, float *hs, void *stream);
+
 /* Replaces the LEAT_KERNELS=ref linear layer, leat/ops.py:35-38 (x @ w.dequant().T with f32
  * activations, not quantized): out[t * rows + r] = W[r] . x[t] (+ residual), W decoded in
  * ggml's operation order, f32 sums. x (tokens, cols) f32; tokens 1..8 or 16. */

@@ -127,6 +127,10 @@ __device__ __forceinline__ float glu(int kind, float g, float u) {
 namespace leat {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+// weights and activation words aligned as the kernels read them (matvec.hip)
+int check_ptrs(int type, const void* w, const void* xq);
+// a row length of whole decode tasks of `type` (matvec.hip)
+int check_cols(int type, int cols);
 }  // namespace leat
 
 #define LEAT_REQUIRE(cond, ...)          \

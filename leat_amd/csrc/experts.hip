@@ -209,9 +209,6 @@ __global__ __launch_bounds__(256) void experts_down_kernel(ExpertsDownArgs a) {
     }
 }
 
-int check_ptrs(int type, const void* w, const void* xq);
-int check_cols(int type, int cols);
-
 }  // namespace leat
 
 using namespace leat;

@@ -9,6 +9,7 @@
 // (q, k and v) run in one launch: waves are numbered across them.
 #include "blocks.h"
 #include "mmv.h"
+#include "rows.h"
 
 namespace leat {
 
@@ -193,10 +194,25 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
 #define LEAT_MMV_MIN_TOKENS 3  // the fewest tokens the matrix-core path takes
 #endif
 
-// the matrix-core path where it fits the shape, else the v_dot4 kernels
+// one or two tokens: the row-streaming kernels; more: the matrix-core path where it fits the
+// shape; else the v_dot4 kernels
 template <int MODE>
 static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     const int nw = MODE == MODE_GLU ? 2 : a.count;
+    if (rows_fits(type, a.cols, tokens)) {
+        RowsArgs r = {};
+        for (int i = 0; i < MAX_MATS; i++) {
+            r.w[i] = a.w[i];
+            r.out[i] = a.out[i];
+            r.rows[i] = a.rows[i];
+        }
+        r.count = a.count;
+        r.cols = a.cols;
+        r.xq = a.xq, r.xd = a.xd, r.xs = a.xs;
+        r.residual = a.residual;
+        r.kind = a.kind;
+        return rows_launch(type, MODE, r, tokens, false, s);
+    }
     if (tokens >= LEAT_MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
         MmvArgs m = {};
         for (int i = 0; i < MAX_MATS; i++) {

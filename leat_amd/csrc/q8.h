@@ -1,0 +1,111 @@
+// The activation quantizer's arithmetic (leat/kernels/quantize.py:25-49), shared by the
+// standalone quantizer and the kernels that quantize their own input, so that every path gives
+// the same bits:
+//   per group of 32 values  d = max|x| / 127,  q = roundf(x / d) (0 where d = 0),  s = d * sum(q)
+// with both quotients IEEE f32 divisions and roundf rounding half away from zero. The values are
+// packed four to an int32 word, byte i of word w holding value 4w + i.
+//
+// Layout of the work: a 256-thread block takes a row 1024 values at a time, thread `tid` the 4
+// consecutive values at 4 * tid, so the 8 threads of an aligned octet hold one group of 32.
+#pragma once
+
+#include "common.h"
+
+namespace leat {
+
+// 1 / sqrt(mean(x^2) + eps) over the n values of row xr, the same in every thread of a block of
+// THREADS >= 256 threads (n a multiple of 4). `partial` is THREADS / 64 floats of the block's
+// shared memory. The summation order is that of a 256-thread block whatever THREADS is, so every
+// kernel normalizes to the same bits: threads 0..255 sum float4 runs strided by 1024, each wave
+// reduces with DPP moves (wave_sum_dpp), then (w0 + w1) + (w2 + w3); further waves contribute nothing.
+template <int THREADS = 256>
+__device__ __forceinline__ float block_inv_rms(const float* __restrict__ xr, int n, float eps, float* partial) {
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+    if (tid < 256)
+        for (int at = tid * 4; at < n; at += 1024) {
+            const float4 v = *(const float4*)(xr + at);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    ss = wave_sum_dpp(ss);
+    __syncthreads();  // `partial` may still be read from a previous row
+    if ((tid & (WAVE - 1)) == 0) partial[tid / WAVE] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    return 1.0f / sqrtf(total / (float)n + eps);
+}
+
+// v of a lane's aligned octet of lanes combined with `op` over the octet, by DPP lane moves (no
+// LDS traffic): xor 1 and xor 2 within quads, then xor 4 as a left shift by 4 into banks 0 and 2
+// of each row of 16 and a right shift by 4 into banks 1 and 3
+template <typename Op>
+__device__ __forceinline__ float octet_reduce(float v, Op op) {
+    v = op(v, LEAT_DPP(v, 0xB1, 0xF, 0xF));  // quad_perm [1,0,3,2]
+    v = op(v, LEAT_DPP(v, 0x4E, 0xF, 0xF));  // quad_perm [2,3,0,1]
+    const int bits = __builtin_bit_cast(int, v);
+    int other = __builtin_amdgcn_update_dpp(bits, bits, 0x104, 0xF, 0x5, false);  // row_shl:4, banks 0, 2
+    other = __builtin_amdgcn_update_dpp(other, bits, 0x114, 0xF, 0xA, false);      // row_shr:4, banks 1, 3
+    return op(v, __builtin_bit_cast(float, other));
+}
+
+// roundf(v / scale) (IEEE quotient, halves away from zero) for scale > 0, from a reciprocal:
+// with r = rcp(scale) (within 1 ulp) the product a = v * r is within |v / scale| * 2^-21 <= 7e-5
+// of the correctly rounded quotient (|v / scale| <= 127 here), so both round to the same integer
+// unless a lies within that of a half-integer; those rare values, and scales too small for the
+// reciprocal, take the division itself.
+__device__ __forceinline__ int round_quotient(float v, float scale, float r) {
+    const float a = v * r;
+    const float frac = fabsf(a - truncf(a));
+    if (fabsf(frac - 0.5f) < 1e-4f || !(scale > 1e-30f)) return (int)roundf(v / scale);
+    return (int)rintf(a);
+}
+
+// Quantizes the 4 values v (positions 4 * (tid % 8) .. + 3 of their group) together with the
+// other 7 threads of the aligned octet. Returns the packed word; every thread of the octet also
+// gets the group's d and s.
+__device__ __forceinline__ uint32_t quantize4(float4 v, float* d_out, float* s_out) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = octet_reduce(amax, [](float a, float b) { return fmaxf(a, b); });
+    const float scale = amax / 127.0f;
+    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    if (scale > 0.0f) {
+        const float r = __builtin_amdgcn_rcpf(scale);
+        q0 = round_quotient(v.x, scale, r);
+        q1 = round_quotient(v.y, scale, r);
+        q2 = round_quotient(v.z, scale, r);
+        q3 = round_quotient(v.w, scale, r);
+    }
+    // the octet's sum of q: small integers, exact in f32 whatever the order
+    const float total = octet_reduce((float)(q0 + q1 + q2 + q3), [](float a, float b) { return a + b; });
+    *d_out = scale;
+    *s_out = scale * total;
+    return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+           ((uint32_t)(q3 & 0xFF) << 24);
+}
+
+// One row of n values (after RMSNorm when `weight` is set, `inv` its 1/rms) into q words, d and s
+// (pointers to the row's first word and group), by a block of THREADS threads. Any address space.
+template <int THREADS = 256, typename Q, typename F>
+__device__ __forceinline__ void quantize_row(const float* __restrict__ xr, int n, const float* __restrict__ weight,
+                                             float inv, Q* q, F* d, F* s) {
+    const int tid = threadIdx.x;
+    for (int at = tid * 4; at < n; at += 4 * THREADS) {  // n % 32 == 0: an octet is all in or all out
+        float4 v = *(const float4*)(xr + at);
+        if (weight) {
+            const float4 wv = *(const float4*)(weight + at);
+            v.x = v.x * inv * wv.x;
+            v.y = v.y * inv * wv.y;
+            v.z = v.z * inv * wv.z;
+            v.w = v.w * inv * wv.w;
+        }
+        float dv, sv;
+        const uint32_t word = quantize4(v, &dv, &sv);
+        q[at / 4] = word;
+        if ((tid & 7) == 0) {
+            d[at / GROUP] = dv;
+            s[at / GROUP] = sv;
+        }
+    }
+}
+
+}  // namespace leat

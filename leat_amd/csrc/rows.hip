@@ -1,0 +1,418 @@
+// Decode products for one or two tokens, streaming whole rows: y[t, row] = W[row] . x[t], the
+// single-stream (and two-stream) case of leat's matvecs / swiglu (leat/kernels/matvec.py:306-395).
+//
+// Work split: lane l of a wave owns the same tasks of every row (tasks l, l + 64, ...; a task is
+// 32 weights of Q4_K or Q6_K, 64 of Q8_0, as in blocks.h), so it loads its activation words and
+// scales into registers once and reuses them for every row the wave streams. A wave owns RPW
+// consecutive rows (of each matrix of the launch: gate and up for the GLU) and walks them one at
+// a time, the loads of the next rows (up to 4) in flight while the current row is computed. A row's sum
+// is one wave-wide DPP reduction.
+//
+// Activations arrive either quantized (xq, xd, xs, as leat's quantize_q8 writes them) or as f32
+// rows that each workgroup quantizes itself into LDS, with an optional RMSNorm, using the
+// standalone quantizer's arithmetic (q8.h): bit for bit what quantize_q8 followed by the product
+// gives, without the separate launch.
+//
+// The GLU can also quantize its own outputs for the down product that consumes them: a
+// workgroup owns 32 consecutive rows (4 waves x 8), so each of its output groups of 32 is
+// complete in the workgroup, and it writes their q8 words, d and s directly.
+#include "blocks.h"
+#include "q8.h"
+#include "rows.h"
+
+namespace leat {
+
+enum RowsMode : int { ROWS_PLAIN = 0, ROWS_RESIDUAL = 1, ROWS_GLU = 2 };
+
+#ifndef LEAT_ROWS_INTERLEAVE
+#define LEAT_ROWS_INTERLEAVE 1
+#endif
+
+#ifndef LEAT_ROWS_DEPTH
+#define LEAT_ROWS_DEPTH 1  // rows of weight loads a wave has in flight, the one it computes next included
+#endif
+
+// A task's weight bytes, read with 32-bit offsets from the row's (uniform) start.
+template <int TYPE> struct RowTask;
+
+// Q4_K: a lane's task k = task % 8 is the same in every row (task = lane + 64 i), so its
+// sub-block pair j = k / 2 and half h = k % 2 are lane constants, and get_scale_min_k4
+// (leat/quant.py:182-187) for sub-blocks 2j and 2j+1 becomes two masked byte pairs per row:
+//   j < 2:  scales = bytes 2j, 2j+1 of q0 & 63,  mins = the same of q1
+//   j >= 2: scales = (bytes 2j-4, 2j-3 of q2 & 15) | (top 2 bits of those of q0) << 4,
+//           mins   = (the same bytes of q2 >> 4)   | (top 2 bits of those of q1) << 4
+// (q0, q1, q2 the header's scale words). The mins enter once per sub-block, through the h = 0
+// lanes; the h = 1 lanes hold zero activation sums instead of a branch.
+template <>
+struct RowTask<Q4_K> {
+    using Raw = Task<Q4_K>::Raw;
+    struct Off {
+        uint32_t hdr, qs;
+        bool high;                      // sub-blocks 4..7
+        uint32_t sh_sc, sh_m, sh_top;  // shifts of the scale nibbles, the min nibbles, the top bits
+    };
+    __device__ static Off at(int task) {
+        const uint32_t b = (uint32_t)task >> 3, k = (uint32_t)task & 7, j = k >> 1;
+        Off o;
+        o.hdr = b * 144u;
+        o.qs = b * 144u + 16u + 16u * k;
+        o.high = j >= 2;
+        const uint32_t base = 16u * (j & 1);
+        o.sh_sc = base;
+        o.sh_m = o.high ? base + 4 : base;
+        o.sh_top = o.high ? base + 2 : base;
+        return o;
+    }
+    __device__ static Raw load(const uint8_t* row, const Off& o) {
+        Raw r;
+        r.hdr = stream_load((const u32x4*)(row + o.hdr));
+        r.qs = stream_load((const u32x4*)(row + o.qs));
+        return r;
+    }
+    // the lane's activations for the task, with s zeroed on the h = 1 lanes
+    __device__ static ActQ act(ActQ a, int task) {
+        if (task & 1) a.s0 = a.s1 = 0.0f;
+        return a;
+    }
+    // the task's share of the row's product with one token
+    __device__ static float dot(const Raw& r, const Off& o, const ActQ& x) {
+        const uint32_t q0 = r.hdr[1], q1 = r.hdr[2], q2 = r.hdr[3];
+        const uint32_t xs = o.high ? q2 : q0, xm = o.high ? q2 : q1;
+        const uint32_t sc = ((xs >> o.sh_sc) & 0x0F0Fu) | ((q0 >> o.sh_top) & 0x3030u);
+        const uint32_t mn = ((xm >> o.sh_m) & 0x0F0Fu) | ((q1 >> o.sh_top) & 0x3030u);
+        int d0 = 0, d1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            d0 = dot4(r.qs[i] & 0x0F0F0F0Fu, x.x0[i], d0);
+            d1 = dot4((r.qs[i] >> 4) & 0x0F0F0F0Fu, x.x1[i], d1);
+        }
+        const float d = f16_lo(r.hdr[0]), dmin = f16_hi(r.hdr[0]);
+        const float scaled = (float)(sc & 0xFF) * (x.d0 * (float)d0) + (float)(sc >> 8) * (x.d1 * (float)d1);
+        const float mins = (float)(mn & 0xFF) * x.s0 + (float)(mn >> 8) * x.s1;
+        return d * scaled - dmin * mins;
+    }
+};
+
+template <>
+struct RowTask<Q8_0> {
+    using Raw = Task<Q8_0>::Raw;
+    struct Off {
+        uint32_t first;
+    };
+    __device__ static Off at(int task) { return {(uint32_t)task * 68u}; }
+    __device__ static Raw load(const uint8_t* row, const Off& o) {
+        const uint32_t* p = (const uint32_t*)(row + o.first);
+        Raw r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 q = stream_load((const u32x4_a4*)(p + 4 * i));
+            r.v[4 * i] = q[0], r.v[4 * i + 1] = q[1], r.v[4 * i + 2] = q[2], r.v[4 * i + 3] = q[3];
+        }
+        r.v[16] = stream_load(p + 16);
+        return r;
+    }
+    __device__ static ActQ act(ActQ a, int) { return a; }
+    __device__ static float dot(const Raw& r, const Off&, const ActQ& x) {
+        const Task<Q8_0>::Dec dec = Task<Q8_0>::decode(r, 0);
+        return Task<Q8_0>::combine(dec, x, Task<Q8_0>::dots(dec, x));
+    }
+};
+
+// FULL: the row's tasks fill exactly NT turns of the wave, so no lane needs a bounds check
+// WPG waves per workgroup, RPW rows per wave: a workgroup owns a tile of WPG * RPW rows
+template <int TYPE, int B, int NT, int RPW, int WPG, int MODE, bool XF32, bool FULL>
+__global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
+    using T = Task<TYPE>;
+    using RT = RowTask<TYPE>;
+    constexpr int NM = MODE == ROWS_GLU ? 2 : 1;
+    extern __shared__ uint32_t rows_lds[];
+    __shared__ float partial[WPG < 4 ? 4 : WPG];
+    __shared__ float glu_out[B][32];
+
+    const int cols = a.cols, tasks = cols / T::TASK_W;
+    const int lane = threadIdx.x & (WAVE - 1);
+    // the wave's number in the workgroup, known to the compiler as uniform so row addresses stay
+    // scalar. A workgroup owns a tile of WPG * RPW consecutive rows of one matrix; with
+    // LEAT_ROWS_INTERLEAVE its waves take every WPG-th row (w, w + WPG, ...), so at each step the
+    // waves read adjacent rows, else each wave RPW consecutive rows
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int tile = blockIdx.x;
+    int m = 0;
+    if (MODE != ROWS_GLU)
+        while (m + 1 < a.count && tile >= a.tile_start[m + 1]) m++;
+    const int rows = a.rows[m];
+    const int tile_row = (tile - a.tile_start[m]) * WPG * RPW;
+    constexpr int STEP = LEAT_ROWS_INTERLEAVE ? WPG : 1;
+    const int row0 = tile_row + (LEAT_ROWS_INTERLEAVE ? w : RPW * w);
+    const uint32_t row_bytes = (uint32_t)(cols / T::WEIGHTS) * T::BYTES;
+    const uint8_t* wm[NM];
+    wm[0] = a.w[MODE == ROWS_GLU ? 0 : m];
+    if (NM == 2) wm[NM - 1] = a.w[1];
+
+    // the lane's tasks and their offsets in a row
+    typename RT::Off off[NT];
+    bool has[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+        const int task = lane + WAVE * i;
+        has[i] = FULL || task < tasks;
+        off[i] = RT::at(has[i] ? task : 0);
+    }
+
+    // P rows' weights in flight at a time, the first P before the activations are ready
+    constexpr int P = RPW < LEAT_ROWS_DEPTH ? RPW : LEAT_ROWS_DEPTH;
+    typename T::Raw buf[P][NM][NT];
+    auto fetch = [&](typename T::Raw(&dst)[NM][NT], int row) {
+#pragma unroll
+        for (int k = 0; k < NM; k++)
+#pragma unroll
+            for (int i = 0; i < NT; i++)
+                if (has[i]) dst[k][i] = RT::load(wm[k] + (size_t)row * row_bytes, off[i]);
+    };
+#pragma unroll
+    for (int p = 0; p < P; p++)
+        if (row0 + STEP * p < rows) fetch(buf[p], row0 + STEP * p);
+
+    ActQ act[NT][B];
+    if (XF32) {
+        // the workgroup quantizes the tokens' rows into LDS: words, then d, then s
+        const int words = B * (cols / 4), groups = B * (cols / GROUP);
+        float* lds_d = (float*)(rows_lds + words);
+#pragma unroll
+        for (int t = 0; t < B; t++) {
+            const float* xr = a.x + (int64_t)t * cols;
+            const float inv = a.norm ? block_inv_rms<WPG * 64>(xr, cols, a.eps, partial) : 1.0f;
+            quantize_row<WPG * 64>(xr, cols, a.norm, inv, rows_lds + t * (cols / 4), lds_d + t * (cols / GROUP),
+                         lds_d + groups + t * (cols / GROUP));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+#pragma unroll
+            for (int t = 0; t < B; t++)
+                act[i][t] = RT::act(load_act_lds<TYPE>(rows_lds, B, cols, t, has[i] ? lane + WAVE * i : 0), lane);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+#pragma unroll
+            for (int t = 0; t < B; t++)
+                act[i][t] = RT::act(load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, has[i] ? lane + WAVE * i : 0), lane);
+    }
+
+    float keep[RPW][B];  // the GLU's outputs of the wave's rows, for the q8 epilogue
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const int row = row0 + STEP * r;
+        if (row >= rows) break;  // uniform across the wave
+        float acc[NM][B];
+#pragma unroll
+        for (int k = 0; k < NM; k++)
+#pragma unroll
+            for (int t = 0; t < B; t++) acc[k][t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (!has[i]) continue;
+#pragma unroll
+            for (int k = 0; k < NM; k++)
+#pragma unroll
+                for (int t = 0; t < B; t++) acc[k][t] += RT::dot(buf[r % P][k][i], off[i], act[i][t]);
+        }
+        // the slot is free again: the row P further on
+        if (r + P < RPW && row + STEP * P < rows) fetch(buf[r % P], row + STEP * P);
+#pragma unroll
+        for (int t = 0; t < B; t++) {
+            float y = wave_sum_dpp(acc[0][t]);
+            if (MODE == ROWS_GLU) y = glu(a.kind, y, wave_sum_dpp(acc[NM - 1][t]));
+            const int64_t at = (int64_t)t * rows + row;
+            if (MODE == ROWS_RESIDUAL) y += a.residual[at];
+            keep[r][t] = y;
+            float* out = a.out[MODE == ROWS_GLU ? 0 : m];
+            if (lane == 0 && out) out[at] = y;
+        }
+    }
+
+    // the GLU's own outputs quantized: the workgroup's 32 rows are one group per token
+    if (MODE == ROWS_GLU && WPG * RPW == 32 && a.hq) {
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int t = 0; t < B; t++)
+                if (lane == r) glu_out[t][row0 - tile_row + STEP * r] = keep[r][t];
+        __syncthreads();
+        if (threadIdx.x < 32 * B) {
+            const int t = threadIdx.x >> 5, i = threadIdx.x & 31;
+            const float v = glu_out[t][i];
+            float amax = fabsf(v);
+#pragma unroll
+            for (int s = 1; s < 32; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 32));
+            const float scale = amax / 127.0f;
+            const int q = scale > 0.0f ? (int)roundf(v / scale) : 0;
+            int total = q;
+#pragma unroll
+            for (int s = 1; s < 32; s <<= 1) total += __shfl_xor(total, s, 32);
+            // four consecutive lanes' values make a word, value 4w + i in byte i
+            const uint32_t b0 = (uint32_t)(q & 0xFF);
+            const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
+            const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
+            const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
+            const int total_rows = a.rows[0];
+            if ((i & 3) == 0)
+                a.hq[((int64_t)t * total_rows + 32 * tile + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (i == 0) {
+                const int64_t g = ((int64_t)t * total_rows + 32 * tile) / GROUP;
+                a.hd[g] = scale;
+                a.hs[g] = scale * (float)total;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------- launching
+
+template <int TYPE, int B, int NT, int RPW, int WPG, int MODE, bool XF32>
+static int rows_go(RowsArgs& a, hipStream_t st) {
+    const bool full = a.cols / Task<TYPE>::TASK_W == NT * WAVE;
+    int total = 0;  // workgroups: tiles of WPG * RPW rows, per matrix
+    for (int i = 0; i < a.count; i++) {
+        a.tile_start[i] = total;
+        total += (a.rows[i] + WPG * RPW - 1) / (WPG * RPW);
+    }
+    a.tile_start[a.count] = total;
+    const size_t lds = XF32 ? (size_t)B * a.cols + 2 * (size_t)B * (a.cols / GROUP) * 4 : 0;
+    if (full)
+        hipLaunchKernelGGL((rows_kernel<TYPE, B, NT, RPW, WPG, MODE, XF32, true>), dim3(total), dim3(WPG * 64), lds,
+                           st, a);
+    else
+        hipLaunchKernelGGL((rows_kernel<TYPE, B, NT, RPW, WPG, MODE, XF32, false>), dim3(total), dim3(WPG * 64), lds,
+                           st, a);
+    return check_launch("rows");
+}
+
+#ifndef LEAT_ROWS_RPW
+#define LEAT_ROWS_RPW 2  // rows a wave streams in the plain and residual products
+#endif
+#ifndef LEAT_ROWS_WPG
+#define LEAT_ROWS_WPG 8  // waves per workgroup in the plain and residual products
+#endif
+#ifndef LEAT_ROWS_GLU_WPG
+#define LEAT_ROWS_GLU_WPG 8  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
+#endif
+
+template <int TYPE, int B, int NT, int MODE>
+static int rows_shape(RowsArgs& a, bool xf32, hipStream_t st) {
+    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : LEAT_ROWS_WPG;
+    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : LEAT_ROWS_RPW;
+    return xf32 ? rows_go<TYPE, B, NT, RPW, WPG, MODE, true>(a, st) : rows_go<TYPE, B, NT, RPW, WPG, MODE, false>(a, st);
+}
+
+template <int TYPE, int B, int MODE>
+static int rows_nt(RowsArgs& a, bool xf32, hipStream_t st) {
+    const int tasks = a.cols / Task<TYPE>::TASK_W;
+    if (tasks <= WAVE) return rows_shape<TYPE, B, 1, MODE>(a, xf32, st);
+    if (tasks <= 2 * WAVE) return rows_shape<TYPE, B, 2, MODE>(a, xf32, st);
+    return rows_shape<TYPE, B, 4, MODE>(a, xf32, st);
+}
+
+template <int TYPE, int MODE>
+static int rows_b(RowsArgs& a, int tokens, bool xf32, hipStream_t st) {
+    return tokens == 1 ? rows_nt<TYPE, 1, MODE>(a, xf32, st) : rows_nt<TYPE, 2, MODE>(a, xf32, st);
+}
+
+bool rows_fits(int type, int cols, int tokens) {
+#ifdef LEAT_ROWS_OFF  // build without the row-streaming path (for comparisons)
+    return false;
+#endif
+    if (tokens < 1 || tokens > ROWS_MAX_TOKENS) return false;
+    if (type == Q4_K) return cols % 256 == 0 && cols / 32 <= 4 * WAVE;
+    if (type == Q8_0) return cols % 64 == 0 && cols / 64 <= 2 * WAVE;
+    return false;
+}
+
+int rows_launch(int type, int mode, RowsArgs& a, int tokens, bool xf32, hipStream_t st) {
+#define LEAT_ROWS_MODES(T)                                                  \
+    switch (mode) {                                                         \
+    case ROWS_PLAIN: return rows_b<T, ROWS_PLAIN>(a, tokens, xf32, st);       \
+    case ROWS_RESIDUAL: return rows_b<T, ROWS_RESIDUAL>(a, tokens, xf32, st); \
+    default: return rows_b<T, ROWS_GLU>(a, tokens, xf32, st);                 \
+    }
+    switch (type) {
+    case Q4_K: LEAT_ROWS_MODES(Q4_K)
+    case Q8_0: LEAT_ROWS_MODES(Q8_0)
+    default: set_error("rows: unsupported type %d", type); return -1;
+    }
+#undef LEAT_ROWS_MODES
+}
+
+}  // namespace leat
+
+// ------------------------------------------------------------------------------- the C ABI
+
+using namespace leat;
+
+static int rows_f32_check(int type, int cols, const float* x, int tokens) {
+    if (check_cols(type, cols)) return -1;
+    LEAT_REQUIRE(x, "null activations");
+    LEAT_REQUIRE(rows_fits(type, cols, tokens),
+                 "type %d, %d columns, %d tokens: the kernels that quantize their own input take Q4_K and Q8_0 rows "
+                 "of at most 8192 (Q4_K) or 16384 (Q8_0) weights and 1..%d tokens",
+                 type, cols, tokens, ROWS_MAX_TOKENS);
+    LEAT_REQUIRE((uintptr_t)x % 16 == 0 && cols % 4 == 0, "f32 activations must start 16-byte aligned");
+    return 0;
+}
+
+extern "C" int leat_matvecs_f32(int count, const int* types, const void* const* ws, const int* rows, int cols,
+                                const float* x, int tokens, const float* norm_weight, float eps, float* const* outs,
+                                void* stream) {
+    LEAT_REQUIRE(count >= 1 && count <= ROWS_MATS, "matvecs_f32: 1..%d matrices", ROWS_MATS);
+    RowsArgs a = {};
+    for (int i = 0; i < count; i++) {
+        LEAT_REQUIRE(types[i] == types[0], "matvecs_f32: the matrices of one call share a type");
+        LEAT_REQUIRE(ws[i] && outs[i] && rows[i] > 0, "matvecs_f32: bad matrix %d", i);
+        if (check_ptrs(types[i], ws[i], nullptr)) return -1;
+        a.w[i] = (const uint8_t*)ws[i];
+        a.out[i] = outs[i];
+        a.rows[i] = rows[i];
+    }
+    if (rows_f32_check(types[0], cols, x, tokens)) return -1;
+    LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "matvecs_f32: norm weight not 16-byte aligned");
+    a.count = count, a.cols = cols;
+    a.x = x, a.norm = norm_weight, a.eps = eps;
+    return rows_launch(types[0], ROWS_PLAIN, a, tokens, true, (hipStream_t)stream);
+}
+
+extern "C" int leat_matvec_f32(int type, const void* w, int rows, int cols, const float* x, int tokens,
+                               const float* norm_weight, float eps, const float* residual, float* out, void* stream) {
+    LEAT_REQUIRE(w && out && rows > 0, "matvec_f32: null pointer or empty matrix");
+    if (check_ptrs(type, w, nullptr) || rows_f32_check(type, cols, x, tokens)) return -1;
+    LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "matvec_f32: norm weight not 16-byte aligned");
+    RowsArgs a = {};
+    a.w[0] = (const uint8_t*)w;
+    a.out[0] = out;
+    a.rows[0] = rows;
+    a.count = 1, a.cols = cols;
+    a.x = x, a.norm = norm_weight, a.eps = eps;
+    a.residual = residual;
+    return rows_launch(type, residual ? ROWS_RESIDUAL : ROWS_PLAIN, a, tokens, true, (hipStream_t)stream);
+}
+
+extern "C" int leat_glu_matvec_f32(int type, const void* gate, const void* up, int rows, int cols, const float* x,
+                                   int tokens, const float* norm_weight, float eps, int kind, float* out, int32_t* hq,
+                                   float* hd, float* hs, void* stream) {
+    LEAT_REQUIRE(gate && up && rows > 0, "glu_matvec_f32: null pointer or empty matrix");
+    LEAT_REQUIRE(out || hq, "glu_matvec_f32: neither f32 nor q8 output");
+    LEAT_REQUIRE(!hq || (hd && hs && rows % 32 == 0), "glu_matvec_f32: a q8 output needs d, s and rows in 32s");
+    LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matvec_f32: unknown GLU kind %d", kind);
+    if (check_ptrs(type, gate, nullptr) || check_ptrs(type, up, nullptr) || rows_f32_check(type, cols, x, tokens))
+        return -1;
+    LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "glu_matvec_f32: norm weight not 16-byte aligned");
+    RowsArgs a = {};
+    a.w[0] = (const uint8_t*)gate;
+    a.w[1] = (const uint8_t*)up;
+    a.out[0] = out;
+    a.rows[0] = rows;
+    a.count = 1, a.cols = cols;
+    a.x = x, a.norm = norm_weight, a.eps = eps;
+    a.kind = kind;
+    a.hq = (uint32_t*)hq, a.hd = hd, a.hs = hs;
+    return rows_launch(type, ROWS_GLU, a, tokens, true, (hipStream_t)stream);
+}

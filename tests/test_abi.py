@@ -69,3 +69,22 @@ def test_product_path_has_no_cpu_fallback():
 
     with pytest.raises(_lib.LeatError):
         kernels.quantize_q8(torch.zeros(1, 64))
+
+
+def _parameter_counts() -> dict[str, int]:
+    # name -> number of parameters of each function include/leatmi.h declares
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    counts = {}
+    for name, params in re.findall(r"\b(leat_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        counts[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return counts
+
+
+def test_binding_argument_counts_match_the_header():
+    from leat_amd import _lib
+
+    counts = _parameter_counts()
+    for name, args in _lib.SIGNATURES.items():
+        assert name in counts, f"{name} is bound but not declared"
+        assert len(args) == counts[name], name
