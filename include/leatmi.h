@@ -65,7 +65,8 @@ int leat_glu_matvec(int type, const void *gate, const void *up, int rows, int co
  * and the products, in one launch. Each workgroup quantizes x itself with leat_quantize_q8's
  * arithmetic, so the outputs are bit-identical to leat_quantize_q8 followed by leat_matvecs.
  * x (tokens, cols) f32, 16-byte aligned; 1 to 4 matrices of one type, Q4_K (cols a multiple of
- * 256, at most 8192) or Q8_0 (a multiple of 64, at most 8192); tokens 1 or 2. */
+ * 256, at most 8192), Q8_0 (a multiple of 64, at most 8192) or Q6_K (a multiple of 512, at most
+ * 8192); tokens 1 or 2. */
 int leat_matvecs_f32(int count, const int *types, const void *const *ws, const int *rows, int cols,
                      const float *x, int tokens, const float *norm_weight, float eps,
                      float *const *outs, void *stream);

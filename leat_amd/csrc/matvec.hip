@@ -199,7 +199,7 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
 template <int MODE>
 static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     const int nw = MODE == MODE_GLU ? 2 : a.count;
-    if (rows_fits(type, a.cols, tokens)) {
+    if (rows_fits(type, a.cols, tokens, MODE == MODE_GLU)) {
         RowsArgs r = {};
         for (int i = 0; i < MAX_MATS; i++) {
             r.w[i] = a.w[i];

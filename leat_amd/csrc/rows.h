@@ -30,8 +30,9 @@ struct RowsArgs {
     float* hs;
 };
 
-// whether the row-streaming kernels take this type, row length and token count
-bool rows_fits(int type, int cols, int tokens);
+// whether the row-streaming kernels take this type, row length and token count (glu: for the
+// gate+up GLU, which takes shorter rows)
+bool rows_fits(int type, int cols, int tokens, bool glu);
 // mode: 0 plain (up to ROWS_MATS matrices), 1 residual, 2 gate+up GLU; xf32: quantize a.x
 int rows_launch(int type, int mode, RowsArgs& a, int tokens, bool xf32, hipStream_t st);
 

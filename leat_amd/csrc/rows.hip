@@ -46,6 +46,7 @@ template <int TYPE> struct RowTask;
 template <>
 struct RowTask<Q4_K> {
     using Raw = Task<Q4_K>::Raw;
+    static constexpr uint32_t STRIDE = 8 * 144;  // bytes from a lane's task i to its task i + 1
     struct Off {
         uint32_t hdr, qs;
         bool high;                      // sub-blocks 4..7
@@ -93,9 +94,89 @@ struct RowTask<Q4_K> {
     }
 };
 
+// Q6_K: 210-byte blocks, so within a row a block starts 2 bytes off a 4-byte boundary when its
+// index is odd; a lane's task (and so that alignment) is the same in every row. Each 16-byte run
+// (ql, qh) is read as 5 aligned dwords and realigned. The 6-bit values enter the dot products
+// unsigned (0..63) and the q - 32 of leat/quant.py:213-223 comes back as 32 * (sum of the
+// activations), a lane constant computed once.
+template <>
+struct RowTask<Q6_K> {
+    static constexpr uint32_t STRIDE = 8 * 210;  // a multiple of 4: every task of a lane aligns alike
+    struct Raw {
+        uint32_t ql[5], qh[5];
+        uint32_t sc0, sc1;  // the task's two int8 scales, as bytes
+        uint32_t dword;     // the dword holding d
+    };
+    struct Off {
+        uint32_t ql, qh, sc0, sc1, dword;  // dword-aligned runs, scale bytes
+        uint32_t shift;                    // bytes to realign the runs: 0 or 2
+        bool d_high;                       // d in the upper half of its dword
+        uint32_t sh0, sh1;                 // qh bit shifts of the task's rows kk and kk + 2
+    };
+    __device__ static Off at(int task) {
+        const uint32_t b = (uint32_t)task >> 3, k = (uint32_t)task & 7;
+        const uint32_t n = k >> 2, kk = (k >> 1) & 1, a = k & 1;
+        const uint32_t blk = 210u * b;
+        Off o;
+        o.shift = blk & 3u;  // 0 or 2
+        o.ql = (blk + 64 * n + 32 * kk + 16 * a) & ~3u;
+        o.qh = (blk + 128 + 32 * n + 16 * a) & ~3u;
+        o.sc0 = blk + 192 + 8 * n + 2 * kk + a;
+        o.sc1 = o.sc0 + 4;
+        o.dword = (blk + 208) & ~3u;
+        o.d_high = ((blk + 208) & 2u) != 0;
+        o.sh0 = 2 * kk;
+        o.sh1 = 2 * kk + 4;
+        return o;
+    }
+    __device__ static Raw load(const uint8_t* row, const Off& o) {
+        Raw r;
+        const u32x4 a = stream_load((const u32x4_a4*)(row + o.ql));
+        const u32x4 c = stream_load((const u32x4_a4*)(row + o.qh));
+        r.ql[0] = a[0], r.ql[1] = a[1], r.ql[2] = a[2], r.ql[3] = a[3];
+        r.qh[0] = c[0], r.qh[1] = c[1], r.qh[2] = c[2], r.qh[3] = c[3];
+        r.ql[4] = stream_load((const uint32_t*)(row + o.ql + 16));
+        r.qh[4] = stream_load((const uint32_t*)(row + o.qh + 16));
+        r.sc0 = row[o.sc0];
+        r.sc1 = row[o.sc1];
+        r.dword = stream_load((const uint32_t*)(row + o.dword));
+        return r;
+    }
+    // the activations, with each span's 32 * sum in s0 and s1 (integer bits)
+    __device__ static ActQ act(ActQ a, int) {
+        int sum0 = 0, sum1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sum0 = dot4(0x01010101u, a.x0[i], sum0);
+            sum1 = dot4(0x01010101u, a.x1[i], sum1);
+        }
+        a.s0 = __builtin_bit_cast(float, 32 * sum0);
+        a.s1 = __builtin_bit_cast(float, 32 * sum1);
+        return a;
+    }
+    __device__ static float dot(const Raw& r, const Off& o, const ActQ& x) {
+        int d0 = 0, d1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t ql = align_bytes(r.ql[i + 1], r.ql[i], o.shift);
+            const uint32_t qh = align_bytes(r.qh[i + 1], r.qh[i], o.shift);
+            const uint32_t w0 = (ql & 0x0F0F0F0Fu) | (((qh >> o.sh0) & 0x03030303u) << 4);
+            const uint32_t w1 = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> o.sh1) & 0x03030303u) << 4);
+            d0 = dot4(w0, x.x0[i], d0);
+            d1 = dot4(w1, x.x1[i], d1);
+        }
+        d0 -= __builtin_bit_cast(int, x.s0);
+        d1 -= __builtin_bit_cast(int, x.s1);
+        const float d = o.d_high ? f16_hi(r.dword) : f16_lo(r.dword);
+        const float s0 = (float)(int8_t)r.sc0, s1 = (float)(int8_t)r.sc1;
+        return d * (x.d0 * s0 * (float)d0 + x.d1 * s1 * (float)d1);
+    }
+};
+
 template <>
 struct RowTask<Q8_0> {
     using Raw = Task<Q8_0>::Raw;
+    static constexpr uint32_t STRIDE = 64 * 68;
     struct Off {
         uint32_t first;
     };
@@ -149,31 +230,30 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     wm[0] = a.w[MODE == ROWS_GLU ? 0 : m];
     if (NM == 2) wm[NM - 1] = a.w[1];
 
-    // the lane's tasks and their offsets in a row
-    typename RT::Off off[NT];
+    // the lane's tasks: lane + 64 i, each RT::STRIDE bytes past the previous in a row, so one set
+    // of offsets (those of task `lane`) serves them all
+    const typename RT::Off off = RT::at(lane);
     bool has[NT];
 #pragma unroll
-    for (int i = 0; i < NT; i++) {
-        const int task = lane + WAVE * i;
-        has[i] = FULL || task < tasks;
-        off[i] = RT::at(has[i] ? task : 0);
-    }
+    for (int i = 0; i < NT; i++) has[i] = FULL || lane + WAVE * i < tasks;
 
     // P rows' weights in flight at a time, the first P before the activations are ready
     constexpr int P = RPW < LEAT_ROWS_DEPTH ? RPW : LEAT_ROWS_DEPTH;
-    typename T::Raw buf[P][NM][NT];
-    auto fetch = [&](typename T::Raw(&dst)[NM][NT], int row) {
+    typename RT::Raw buf[P][NM][NT];
+    auto fetch = [&](typename RT::Raw(&dst)[NM][NT], int row) {
 #pragma unroll
         for (int k = 0; k < NM; k++)
 #pragma unroll
             for (int i = 0; i < NT; i++)
-                if (has[i]) dst[k][i] = RT::load(wm[k] + (size_t)row * row_bytes, off[i]);
+                if (has[i]) dst[k][i] = RT::load(wm[k] + (size_t)row * row_bytes + RT::STRIDE * i, off);
     };
 #pragma unroll
     for (int p = 0; p < P; p++)
         if (row0 + STEP * p < rows) fetch(buf[p], row0 + STEP * p);
 
-    ActQ act[NT][B];
+    // The activations: in registers, or for long rows (NT > 4) in LDS, read again for every row,
+    // with only RT::act's lane constants (Q6_K's offset sums) kept in registers
+    constexpr bool ACT_LDS = NT > 4;
     if (XF32) {
         // the workgroup quantizes the tokens' rows into LDS: words, then d, then s
         const int words = B * (cols / 4), groups = B * (cols / GROUP);
@@ -183,21 +263,31 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
             const float* xr = a.x + (int64_t)t * cols;
             const float inv = a.norm ? block_inv_rms<WPG * 64>(xr, cols, a.eps, partial) : 1.0f;
             quantize_row<WPG * 64>(xr, cols, a.norm, inv, rows_lds + t * (cols / 4), lds_d + t * (cols / GROUP),
-                         lds_d + groups + t * (cols / GROUP));
+                                   lds_d + groups + t * (cols / GROUP));
         }
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < NT; i++)
-#pragma unroll
-            for (int t = 0; t < B; t++)
-                act[i][t] = RT::act(load_act_lds<TYPE>(rows_lds, B, cols, t, has[i] ? lane + WAVE * i : 0), lane);
-    } else {
-#pragma unroll
-        for (int i = 0; i < NT; i++)
-#pragma unroll
-            for (int t = 0; t < B; t++)
-                act[i][t] = RT::act(load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, has[i] ? lane + WAVE * i : 0), lane);
+    } else if (ACT_LDS) {
+        // q8 input staged: words, then d, then s (Q4_K only)
+        const int words = B * (cols / 4), groups = B * (cols / GROUP);
+        for (int i = threadIdx.x; i < words / 4; i += WPG * 64)
+            ((u32x4*)rows_lds)[i] = ((const u32x4*)a.xq)[i];
+        float* lds_d = (float*)(rows_lds + words);
+        for (int i = threadIdx.x; i < groups; i += WPG * 64) {
+            lds_d[i] = a.xd[i];
+            if (TYPE == Q4_K) lds_d[groups + i] = a.xs[i];
+        }
+        __syncthreads();
     }
+    auto fresh = [&](int i, int t, const uint32_t* lds) -> ActQ {
+        const int task = has[i] ? lane + WAVE * i : 0;
+        return XF32 || ACT_LDS ? load_act_lds<TYPE>(lds, B, cols, t, task)
+                               : load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, task);
+    };
+    ActQ act[NT][B];
+#pragma unroll
+    for (int i = 0; i < NT; i++)
+#pragma unroll
+        for (int t = 0; t < B; t++) act[i][t] = RT::act(fresh(i, t, rows_lds), lane);
 
     float keep[RPW][B];  // the GLU's outputs of the wave's rows, for the q8 epilogue
 #pragma unroll
@@ -209,13 +299,27 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
         for (int k = 0; k < NM; k++)
 #pragma unroll
             for (int t = 0; t < B; t++) acc[k][t] = 0.0f;
+        // the LDS activations' base, opaque to the compiler so it reads them again for each row
+        // rather than holding all of them in registers
+        const uint32_t* lds_row = rows_lds;
+        if (ACT_LDS) asm volatile("" : "+v"(lds_row));
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (!has[i]) continue;
 #pragma unroll
             for (int k = 0; k < NM; k++)
 #pragma unroll
-                for (int t = 0; t < B; t++) acc[k][t] += RT::dot(buf[r % P][k][i], off[i], act[i][t]);
+                for (int t = 0; t < B; t++) {
+                    ActQ x = act[i][t];
+                    if (ACT_LDS) {  // the words and scales again from LDS, the lane constants kept
+                        const ActQ again = fresh(i, t, lds_row);
+                        x.d0 = again.d0, x.d1 = again.d1;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) x.x0[j] = again.x0[j], x.x1[j] = again.x1[j];
+                        if (TYPE == Q4_K) x.s0 = again.s0, x.s1 = again.s1;
+                    }
+                    acc[k][t] += RT::dot(buf[r % P][k][i], off, x);
+                }
         }
         // the slot is free again: the row P further on
         if (r + P < RPW && row + STEP * P < rows) fetch(buf[r % P], row + STEP * P);
@@ -278,7 +382,7 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
         total += (a.rows[i] + WPG * RPW - 1) / (WPG * RPW);
     }
     a.tile_start[a.count] = total;
-    const size_t lds = XF32 ? (size_t)B * a.cols + 2 * (size_t)B * (a.cols / GROUP) * 4 : 0;
+    const size_t lds = XF32 || NT > 4 ? (size_t)B * a.cols + 2 * (size_t)B * (a.cols / GROUP) * 4 : 0;
     if (full)
         hipLaunchKernelGGL((rows_kernel<TYPE, B, NT, RPW, WPG, MODE, XF32, true>), dim3(total), dim3(WPG * 64), lds,
                            st, a);
@@ -294,14 +398,21 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
 #ifndef LEAT_ROWS_WPG
 #define LEAT_ROWS_WPG 8  // waves per workgroup in the plain and residual products
 #endif
+#ifndef LEAT_ROWS_LONG
+#define LEAT_ROWS_LONG 0  // take rows of more than 256 tasks (Q6_K 14336) on these kernels
+#endif
+#ifndef LEAT_ROWS_LONG_WPG
+#define LEAT_ROWS_LONG_WPG 4  // waves per workgroup for rows of more than 256 tasks (Q6_K 14336)
+#endif
 #ifndef LEAT_ROWS_GLU_WPG
 #define LEAT_ROWS_GLU_WPG 8  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
 #endif
 
 template <int TYPE, int B, int NT, int MODE>
 static int rows_shape(RowsArgs& a, bool xf32, hipStream_t st) {
-    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : LEAT_ROWS_WPG;
-    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : LEAT_ROWS_RPW;
+    // long rows (seven tasks a lane) one row a wave: their loads alone fill the registers
+    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : NT > 4 ? LEAT_ROWS_LONG_WPG : LEAT_ROWS_WPG;
+    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : NT > 4 ? 1 : LEAT_ROWS_RPW;
     return xf32 ? rows_go<TYPE, B, NT, RPW, WPG, MODE, true>(a, st) : rows_go<TYPE, B, NT, RPW, WPG, MODE, false>(a, st);
 }
 
@@ -310,6 +421,14 @@ static int rows_nt(RowsArgs& a, bool xf32, hipStream_t st) {
     const int tasks = a.cols / Task<TYPE>::TASK_W;
     if (tasks <= WAVE) return rows_shape<TYPE, B, 1, MODE>(a, xf32, st);
     if (tasks <= 2 * WAVE) return rows_shape<TYPE, B, 2, MODE>(a, xf32, st);
+    if (tasks > 4 * WAVE) {  // Q6_K rows up to 14336 weights; not for the GLU (rows_fits)
+        if constexpr (MODE == ROWS_GLU) {
+            set_error("rows: GLU rows of %d tasks", tasks);
+            return -1;
+        } else {
+            return rows_shape<TYPE, B, 7, MODE>(a, xf32, st);
+        }
+    }
     return rows_shape<TYPE, B, 4, MODE>(a, xf32, st);
 }
 
@@ -318,13 +437,18 @@ static int rows_b(RowsArgs& a, int tokens, bool xf32, hipStream_t st) {
     return tokens == 1 ? rows_nt<TYPE, 1, MODE>(a, xf32, st) : rows_nt<TYPE, 2, MODE>(a, xf32, st);
 }
 
-bool rows_fits(int type, int cols, int tokens) {
+bool rows_fits(int type, int cols, int tokens, bool glu) {
 #ifdef LEAT_ROWS_OFF  // build without the row-streaming path (for comparisons)
     return false;
 #endif
     if (tokens < 1 || tokens > ROWS_MAX_TOKENS) return false;
     if (type == Q4_K) return cols % 256 == 0 && cols / 32 <= 4 * WAVE;
     if (type == Q8_0) return cols % 64 == 0 && cols / 64 <= 2 * WAVE;
+    // Q6_K rows of whole block pairs (4-byte aligned rows), up to 14336 weights; only with q8 input
+    // Q6_K rows of whole 512s: up to 8192 weights; longer ones (seven tasks a lane, supported below
+    // with the activations in LDS) measured slower than the v_dot4 kernel at 14336, so they stay off
+    // unless LEAT_ROWS_LONG is set
+    if (type == Q6_K) return cols % 512 == 0 && cols / 32 <= (glu || !LEAT_ROWS_LONG ? 4 : 7) * WAVE;
     return false;
 }
 
@@ -337,6 +461,7 @@ int rows_launch(int type, int mode, RowsArgs& a, int tokens, bool xf32, hipStrea
     }
     switch (type) {
     case Q4_K: LEAT_ROWS_MODES(Q4_K)
+    case Q6_K: LEAT_ROWS_MODES(Q6_K)
     case Q8_0: LEAT_ROWS_MODES(Q8_0)
     default: set_error("rows: unsupported type %d", type); return -1;
     }
@@ -349,12 +474,12 @@ int rows_launch(int type, int mode, RowsArgs& a, int tokens, bool xf32, hipStrea
 
 using namespace leat;
 
-static int rows_f32_check(int type, int cols, const float* x, int tokens) {
+static int rows_f32_check(int type, int cols, const float* x, int tokens, bool glu) {
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(x, "null activations");
-    LEAT_REQUIRE(rows_fits(type, cols, tokens),
+    LEAT_REQUIRE(rows_fits(type, cols, tokens, glu),
                  "type %d, %d columns, %d tokens: the kernels that quantize their own input take Q4_K and Q8_0 rows "
-                 "of at most 8192 (Q4_K) or 16384 (Q8_0) weights and 1..%d tokens",
+                 "of at most 8192 weights, Q6_K rows of whole 512s up to 8192, and 1..%d tokens",
                  type, cols, tokens, ROWS_MAX_TOKENS);
     LEAT_REQUIRE((uintptr_t)x % 16 == 0 && cols % 4 == 0, "f32 activations must start 16-byte aligned");
     return 0;
@@ -373,7 +498,7 @@ extern "C" int leat_matvecs_f32(int count, const int* types, const void* const* 
         a.out[i] = outs[i];
         a.rows[i] = rows[i];
     }
-    if (rows_f32_check(types[0], cols, x, tokens)) return -1;
+    if (rows_f32_check(types[0], cols, x, tokens, false)) return -1;
     LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "matvecs_f32: norm weight not 16-byte aligned");
     a.count = count, a.cols = cols;
     a.x = x, a.norm = norm_weight, a.eps = eps;
@@ -383,7 +508,7 @@ extern "C" int leat_matvecs_f32(int count, const int* types, const void* const* 
 extern "C" int leat_matvec_f32(int type, const void* w, int rows, int cols, const float* x, int tokens,
                                const float* norm_weight, float eps, const float* residual, float* out, void* stream) {
     LEAT_REQUIRE(w && out && rows > 0, "matvec_f32: null pointer or empty matrix");
-    if (check_ptrs(type, w, nullptr) || rows_f32_check(type, cols, x, tokens)) return -1;
+    if (check_ptrs(type, w, nullptr) || rows_f32_check(type, cols, x, tokens, false)) return -1;
     LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "matvec_f32: norm weight not 16-byte aligned");
     RowsArgs a = {};
     a.w[0] = (const uint8_t*)w;
@@ -402,7 +527,7 @@ extern "C" int leat_glu_matvec_f32(int type, const void* gate, const void* up, i
     LEAT_REQUIRE(out || hq, "glu_matvec_f32: neither f32 nor q8 output");
     LEAT_REQUIRE(!hq || (hd && hs && rows % 32 == 0), "glu_matvec_f32: a q8 output needs d, s and rows in 32s");
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matvec_f32: unknown GLU kind %d", kind);
-    if (check_ptrs(type, gate, nullptr) || check_ptrs(type, up, nullptr) || rows_f32_check(type, cols, x, tokens))
+    if (check_ptrs(type, gate, nullptr) || check_ptrs(type, up, nullptr) || rows_f32_check(type, cols, x, tokens, true))
         return -1;
     LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "glu_matvec_f32: norm weight not 16-byte aligned");
     RowsArgs a = {};
