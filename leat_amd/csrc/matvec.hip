@@ -10,6 +10,7 @@
 #include "blocks.h"
 #include "mmv.h"
 #include "rows.h"
+#include "tiles.h"
 
 namespace leat {
 
@@ -193,9 +194,12 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
 #ifndef LEAT_MMV_MIN_TOKENS
 #define LEAT_MMV_MIN_TOKENS 3  // the fewest tokens the matrix-core path takes
 #endif
+#ifndef LEAT_TILES
+#define LEAT_TILES 1  // 0: 3..8 tokens take the staged matrix-core kernels instead of the tile kernels
+#endif
 
-// one or two tokens: the row-streaming kernels; more: the matrix-core path where it fits the
-// shape; else the v_dot4 kernels
+// one or two tokens: the row-streaming kernels; 3..8: the matrix-core tile kernels; more (16):
+// the staged matrix-core kernels where they fit the shape; else the v_dot4 kernels
 template <int MODE>
 static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     const int nw = MODE == MODE_GLU ? 2 : a.count;
@@ -212,6 +216,21 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         r.residual = a.residual;
         r.kind = a.kind;
         return rows_launch(type, MODE, r, tokens, false, s);
+    }
+    if (LEAT_TILES && tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
+        TileArgs t = {};
+        for (int i = 0; i < MAX_MATS; i++) {
+            t.w[i] = a.w[i];
+            t.out[i] = a.out[i];
+            t.rows[i] = a.rows[i];
+        }
+        t.count = a.count;
+        t.cols = a.cols;
+        t.tokens = tokens;
+        t.xq = a.xq, t.xd = a.xd, t.xs = a.xs;
+        t.residual = a.residual;
+        t.kind = a.kind;
+        return tiles_launch(type, MODE, t, s);
     }
     if (tokens >= LEAT_MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
         MmvArgs m = {};

@@ -431,6 +431,7 @@ static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
     if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1)
         if (want >= 8 && stages >= 8) return mmv_launch_s<TYPE, MODE, NV, 8>(a, st);
     if (want >= 4 && stages >= 4) return mmv_launch_s<TYPE, MODE, NV, 4>(a, st);
+    if (want >= 2 && stages >= 2) return mmv_launch_s<TYPE, MODE, NV, 2>(a, st);
     return mmv_launch_s<TYPE, MODE, NV, 1>(a, st);
 }
 

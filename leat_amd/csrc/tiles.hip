@@ -1,0 +1,328 @@
+// Decode products for 3..8 tokens of Q4_K weights on matrix cores: y[t, row] = W[row] . x[t],
+// every weight read once for all tokens (leat/kernels/matvec.py:1-4, 306-395 at batch sizes above
+// two). Q6_K's 210-byte blocks, which do not split into aligned 16-byte runs, take the LDS-staged
+// kernels of mmv.hip instead.
+//
+// Work split: a workgroup owns a tile of 32 consecutive rows (of gate and of up for the GLU); its
+// S waves split the rows' blocks between them, each streaming a contiguous run of blocks, and add
+// their sums through LDS at the end.
+//
+// Memory: every lane loads exactly the bytes its MFMA operand needs (row r = lane % 32, half
+// h = lane / 32 of each group of 32 weights) straight into registers, the next block's loads in
+// flight while the current one is computed; the tokens' q8 words are read from global memory (a
+// few KB, hot in the caches) and their scales staged in LDS once per workgroup.
+//
+// Math: v_mfma_i32_32x32x32_i8 with the rows as N (operand B: lane l holds row l % 32) and the
+// tokens as M (operand A: lane l holds token l % 32, zero past the last), K one group of 32. The
+// int32 result in lane l is row l % 32 for tokens 8(v / 4) + 4h + v % 4 of its registers v; with
+// at most 8 tokens the useful ones are v = 0..3, tokens 4h + v, scaled into f32 per group as
+// leat's kernels combine each group's int32 dot (leat/kernels/matvec.py:107-181): lane h takes
+// qs bytes [32j + 16h, +16) of pair j, whose low nibbles are group 2j's values 16h..16h+15 and
+// high nibbles group 2j+1's; acc += d*sc*xd*D - dmin*m*xs.
+// The GLU can also quantize its own outputs (the tile's 32 rows are one group of 32 per token)
+// for the down product, as the one- and two-token kernels do.
+#include "blocks.h"
+#include "tiles.h"
+
+namespace leat {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+extern __shared__ uint32_t tiles_lds[];
+
+constexpr size_t TILES_MAX_LDS = 160 * 1024;  // LDS a workgroup may have on gfx950
+
+__device__ __forceinline__ v16i tiles_mfma(v4i a, u32x4 b) {
+    const v16i zero = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, __builtin_bit_cast(v4i, b), zero, 0, 0, 0);
+}
+
+enum TilesMode : int { TILES_PLAIN = 0, TILES_RESIDUAL = 1, TILES_GLU = 2 };
+
+// A block's bytes for the lane (row r, half h), loaded from the row's start.
+template <int TYPE> struct TileBlock;
+
+template <>
+struct TileBlock<Q4_K> {
+    static constexpr int BYTES = 144;
+    struct Raw {
+        u32x4 hdr;
+        u32x4 qs[4];  // pair j: qs bytes [32j + 16h, +16)
+    };
+    __device__ static Raw load(const uint8_t* row, int b, int h) {
+        const uint8_t* blk = row + 144u * (uint32_t)b;
+        Raw r;
+        r.hdr = stream_load((const u32x4*)blk);
+#pragma unroll
+        for (int j = 0; j < 4; j++) r.qs[j] = stream_load((const u32x4*)(blk + 16 + 32 * j + 16 * h));
+        return r;
+    }
+};
+
+// The tokens' activations: the q8 words of token t, group g at word t * cols / 4 + 8 g in global
+// memory; the scale tables in LDS, group-major, 8 token slots a group (zero past the last token),
+// d then s.
+struct TileActs {
+    const uint32_t* words;  // the lane's (token, half) words: token * cols / 4 + 4 h
+    bool live;              // the lane's token is one of the tokens
+    int d_off, s_off;       // the LDS tables' offsets in floats
+    // operand A of block b's 8 groups: row l % 32 is token l % 32 (zero past the last token), read
+    // from global memory (the few tokens' words stay in the caches). Issued before the next
+    // block's weight loads, so that waiting for them (loads complete in order) does not wait for
+    // those.
+    __device__ void operands(int b, v4i (&xa)[8]) const {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const v4i v = *(const v4i*)(words + 8 * (8 * b + s));
+            const v4i zero = {};
+            xa[s] = live ? v : zero;
+        }
+    }
+    __device__ float4 scales(int off, int g, int h) const {
+        return *(const float4*)((const float*)tiles_lds + off + 8 * g + 4 * h);
+    }
+};
+
+// One block of NM matrices (gate and up for the GLU) for the lane: acc[k][v] += matrix k's share
+// for the tokens 4h + v. Each group's operand A and scale tables are read once for the matrices,
+// whose products are issued back to back.
+template <int TYPE> struct TileCompute;
+
+template <>
+struct TileCompute<Q4_K> {
+    template <int NM>
+    __device__ static void run(const TileBlock<Q4_K>::Raw (&raw)[NM], int b, const v4i (&xa)[8], const TileActs& x,
+                               int h, float (&acc)[NM][4]) {
+        float d[NM], dmin[NM];
+#pragma unroll
+        for (int k = 0; k < NM; k++) d[k] = f16_lo(raw[k].hdr[0]), dmin[k] = f16_hi(raw[k].hdr[0]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int s = 2 * j + e, g = 8 * b + s;
+                const v4i a = xa[s];
+                const float4 xd = x.scales(x.d_off, g, h), xs = x.scales(x.s_off, g, h);
+                v16i D[NM];
+#pragma unroll
+                for (int k = 0; k < NM; k++) {
+                    const u32x4 w = e ? ((raw[k].qs[j] >> 4) & 0x0F0F0F0Fu) : (raw[k].qs[j] & 0x0F0F0F0Fu);
+                    D[k] = tiles_mfma(a, w);
+                }
+#pragma unroll
+                for (int k = 0; k < NM; k++) {
+                    // get_scale_min_k4 (leat/quant.py:182-187), s known at compile time
+                    const uint32_t sh = 8u * (uint32_t)(s & 3);
+                    const uint32_t x0 = raw[k].hdr[1] >> sh, x1 = raw[k].hdr[2] >> sh, x2 = raw[k].hdr[3] >> sh;
+                    const uint32_t scv = s < 4 ? (x0 & 63u) : ((x2 & 15u) | ((x0 >> 2) & 0x30u));
+                    const uint32_t mv = s < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
+                    const float sc = d[k] * (float)scv, mn = dmin[k] * (float)mv;
+                    acc[k][0] += sc * xd.x * (float)D[k][0] - mn * xs.x;
+                    acc[k][1] += sc * xd.y * (float)D[k][1] - mn * xs.y;
+                    acc[k][2] += sc * xd.z * (float)D[k][2] - mn * xs.z;
+                    acc[k][3] += sc * xd.w * (float)D[k][3] - mn * xs.w;
+                }
+            }
+        }
+    }
+};
+
+template <int TYPE, int MODE, int S>
+__global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
+    using TB = TileBlock<TYPE>;
+    constexpr int NM = MODE == TILES_GLU ? 2 : 1;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int r = lane & 31, h = lane >> 5;
+    const int cols = a.cols, tokens = a.tokens, G = cols / GROUP;
+    const int nb = cols / 256;
+    const uint32_t row_bytes = (uint32_t)nb * TB::BYTES;
+
+    const int tile = blockIdx.x;
+    int m = 0;
+    if (MODE != TILES_GLU)
+        while (m + 1 < a.count && tile >= a.tile_start[m + 1]) m++;
+    const int rows = a.rows[m];
+    const int row0 = (tile - a.tile_start[m]) * 32;
+    const int row = min(row0 + r, rows - 1);  // rows past the end repeat the last (never stored)
+    const uint8_t* wr[NM];
+    wr[0] = (MODE == TILES_GLU ? a.w[0] : a.w[m]) + (size_t)row * row_bytes;
+    if (NM == 2) wr[NM - 1] = a.w[1] + (size_t)row * row_bytes;
+
+    // the wave's blocks, and the first one's loads before anything else
+    const int b0 = nb * w / S, b1 = nb * (w + 1) / S;
+    typename TB::Raw cur[NM];
+    if (b0 < b1)
+#pragma unroll
+        for (int k = 0; k < NM; k++) cur[k] = TB::load(wr[k], b0, h);
+
+    // the tokens' scale tables into LDS, group-major: read in the source's order (token-major)
+    TileActs x;
+    x.d_off = 0;
+    x.s_off = 8 * G;
+    {
+        float* tab = (float*)tiles_lds;
+        for (int i = threadIdx.x; i < 8 * G; i += S * 64) {
+            const int t = i / G, g = i - t * G;
+            const bool in = t < tokens;
+            tab[8 * g + t] = in ? a.xd[i] : 0.0f;
+            tab[8 * G + 8 * g + t] = in ? a.xs[i] : 0.0f;
+        }
+        __syncthreads();
+    }
+    x.live = r < tokens;
+    x.words = (const uint32_t*)a.xq + (int64_t)(x.live ? r : 0) * (cols / 4) + 4 * h;
+
+    float acc[NM][4];
+#pragma unroll
+    for (int k = 0; k < NM; k++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[k][v] = 0.0f;
+
+    for (int b = b0; b < b1; b++) {
+        v4i xa[8];
+        x.operands(b, xa);
+        typename TB::Raw nxt[NM];
+        if (b + 1 < b1)
+#pragma unroll
+            for (int k = 0; k < NM; k++) nxt[k] = TB::load(wr[k], b + 1, h);
+        TileCompute<TYPE>::template run<NM>(cur, b, xa, x, h, acc);
+        if (b + 1 < b1)
+#pragma unroll
+            for (int k = 0; k < NM; k++) cur[k] = nxt[k];
+    }
+
+    // the S waves' sums, through LDS (after the activations' last reads)
+    __syncthreads();
+    float* red = (float*)tiles_lds;
+    if (S > 1) {
+#pragma unroll
+        for (int k = 0; k < NM; k++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[((w * NM + k) * 4 + v) * 64 + lane] = acc[k][v];
+        __syncthreads();
+        if (w != 0) return;
+#pragma unroll
+        for (int k = 0; k < NM; k++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float sum = 0.0f;
+                for (int i = 0; i < S; i++) sum += red[((i * NM + k) * 4 + v) * 64 + lane];
+                acc[k][v] = sum;
+            }
+    }
+    // wave 0: lane (r, h) holds row row0 + r for tokens 4h + v
+    const bool row_in = row0 + r < rows;
+    float y[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int t = 4 * h + v;
+        y[v] = acc[0][v];
+        if (MODE == TILES_GLU) y[v] = glu(a.kind, acc[0][v], acc[NM - 1][v]);
+        const int64_t at = (int64_t)t * rows + row0 + r;
+        if (MODE == TILES_RESIDUAL && t < tokens && row_in) y[v] += a.residual[at];
+        float* out = a.out[MODE == TILES_GLU ? 0 : m];
+        if (out && t < tokens && row_in) out[at] = y[v];
+    }
+    // the GLU's outputs quantized: for each token the tile's 32 rows are one group of 32
+    if (MODE == TILES_GLU && a.hq) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int t = 4 * h + v;
+            float amax = fabsf(y[v]);
+#pragma unroll
+            for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
+            const float scale = amax / 127.0f;
+            const int q = scale > 0.0f ? (int)roundf(y[v] / scale) : 0;
+            int total = q;
+#pragma unroll
+            for (int sft = 1; sft < 32; sft <<= 1) total += __shfl_xor(total, sft, 32);
+            const uint32_t b0q = (uint32_t)(q & 0xFF);
+            const uint32_t b1q = (uint32_t)__shfl_down((int)b0q, 1, 32);
+            const uint32_t b2q = (uint32_t)__shfl_down((int)b0q, 2, 32);
+            const uint32_t b3q = (uint32_t)__shfl_down((int)b0q, 3, 32);
+            if (t < tokens) {
+                if ((r & 3) == 0)
+                    a.hq[((int64_t)t * rows + row0 + r) / 4] = b0q | (b1q << 8) | (b2q << 16) | (b3q << 24);
+                if (r == 0) {
+                    const int64_t g = ((int64_t)t * rows + row0) / GROUP;
+                    a.hd[g] = scale;
+                    a.hs[g] = scale * (float)total;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------- launching
+
+#ifndef LEAT_TILES_WAVES
+#define LEAT_TILES_WAVES 2048  // waves a launch aims for
+#endif
+
+template <int TYPE, int MODE, int S>
+static int tiles_go(TileArgs& a, hipStream_t st) {
+    const int tiles = a.tile_start[a.count];
+    const int G = a.cols / GROUP;
+    const size_t acts = (size_t)2 * 8 * G * 4;  // the scale tables
+    const size_t red = (size_t)S * (MODE == TILES_GLU ? 2 : 1) * 4 * 64 * 4;
+    const size_t lds = acts > red ? acts : red;
+    // a workgroup's LDS beyond 64 KB is allowed once per kernel
+    static const hipError_t allowed = hipFuncSetAttribute((const void*)tiles_kernel<TYPE, MODE, S>,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                          (int)TILES_MAX_LDS);
+    if (allowed != hipSuccess && lds > 64 * 1024) {
+        set_error("tiles: %zu bytes of LDS refused", lds);
+        return -1;
+    }
+    hipLaunchKernelGGL((tiles_kernel<TYPE, MODE, S>), dim3(tiles), dim3(S * 64), lds, st, a);
+    return check_launch("tiles");
+}
+
+template <int TYPE, int MODE>
+static int tiles_s(TileArgs& a, hipStream_t st) {
+    const int tiles = a.tile_start[a.count];
+    const int blocks = a.cols / 256;
+    // waves per tile: enough for the launch to fill the GPU, a few blocks each
+    const int want = (LEAT_TILES_WAVES + tiles - 1) / tiles;
+    // (16 waves fit 1024 threads' 128 registers a lane only for the plain products)
+    if constexpr (MODE != TILES_GLU)
+        if (want >= 16 && blocks >= 32) return tiles_go<TYPE, MODE, 16>(a, st);
+    if (want >= 8 && blocks >= 16) return tiles_go<TYPE, MODE, 8>(a, st);
+    if (want >= 4 && blocks >= 8) return tiles_go<TYPE, MODE, 4>(a, st);
+    if (want >= 2 && blocks >= 2) return tiles_go<TYPE, MODE, 2>(a, st);
+    return tiles_go<TYPE, MODE, 1>(a, st);
+}
+
+bool tiles_fits(int type, int cols, int tokens, const void* const* ws, int count) {
+    // Q4_K only: Q6_K's 210-byte blocks load faster staged through LDS (the mmv kernels)
+    if (tokens < 3 || tokens > 8 || type != Q4_K || cols % 256 != 0) return false;
+    // the tokens' scale tables in LDS (160 KB a workgroup on gfx950)
+    if ((size_t)2 * 8 * (cols / GROUP) * 4 > TILES_MAX_LDS) return false;
+    for (int i = 0; i < count; i++)
+        if ((uintptr_t)ws[i] % 16 != 0) return false;
+    return true;
+}
+
+int tiles_launch(int type, int mode, TileArgs& a, hipStream_t st) {
+    int total = 0;
+    for (int i = 0; i < a.count; i++) {
+        a.tile_start[i] = total;
+        total += (a.rows[i] + 31) / 32;
+    }
+    a.tile_start[a.count] = total;
+#define LEAT_TILES_MODES(T)                                                 \
+    switch (mode) {                                                         \
+    case TILES_PLAIN: return tiles_s<T, TILES_PLAIN>(a, st);                \
+    case TILES_RESIDUAL: return tiles_s<T, TILES_RESIDUAL>(a, st);          \
+    default: return tiles_s<T, TILES_GLU>(a, st);                           \
+    }
+    switch (type) {
+    case Q4_K: LEAT_TILES_MODES(Q4_K)
+    default: set_error("tiles: unsupported type %d", type); return -1;
+    }
+#undef LEAT_TILES_MODES
+}
+
+}  // namespace leat
