@@ -109,7 +109,7 @@ int leat_group_dots(int type, const void *w, int rows, int cols, const int32_t *
  * :631-841, with its fixup :856-901) for many tokens: out[t * rows + r] = W[r] . x[t]
  * (+ residual), x as quantize_q8's (xq, xd, xs) for `tokens` rows of `cols`. int8 products per
  * group of 32 on matrix cores, scaled per group in f32. cols a multiple of 256 (512 for Q6_K);
- * weights 4-byte and xq 16-byte aligned. */
+ * weights 4-byte (Q4_K: 16-byte) and xq 16-byte aligned. */
 int leat_matmul(int type, const void *w, int rows, int cols, const int32_t *xq, const float *xd,
                 const float *xs, int tokens, const float *residual, float *out, void *stream);
 

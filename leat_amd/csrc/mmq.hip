@@ -1,15 +1,16 @@
-// Prefill products on matrix cores (leat/kernels/matmul.py: llama.cpp's MMQ): out[t, r] = W[r] .
-// x[t] for many tokens, the activations quantized to int8 per group of 32 as for decode, int32
-// products per group on v_mfma_i32_32x32x32_i8, scaled into f32 per group exactly as leat's
-// _Q4KTile / _Q6KTile / _Q80Tile.scaled (leat/kernels/matmul.py:285-291, 379-387, 447-452).
+// Prefill products of Q6_K and Q8_0 weights on matrix cores (leat/kernels/matmul.py: llama.cpp's
+// MMQ): out[t, r] = W[r] . x[t] for many tokens, the activations quantized to int8 per group of 32
+// as for decode, int32 products per group on v_mfma_i32_32x32x32_i8, scaled into f32 per group
+// exactly as leat's _Q6KTile / _Q80Tile.scaled (leat/kernels/matmul.py:379-387, 447-452). Q4_K
+// takes prefill.hip's kernels.
 //
 // A workgroup owns a tile of 128 tokens by MMQ_TILES row tiles of 32 (of one matrix, or half of
 // gate and the same rows of up); each of its 4 waves owns one 32-token tile for all the row
-// tiles, so the token scales it reads for a group serve MMQ_TILES products. The K loop takes 256 weights a step: a
-// Q4_K or Q6_K block, or 8 Q8_0 blocks per row. Each step the workgroup stages its rows' step
-// bytes (coalesced 16-byte loads, as the decode kernels do) and the 128 tokens' 256 int8 values
-// (row stride padded against bank conflicts) and scales (group-major) in LDS, and loads the next
-// step's bytes into registers while this one is multiplied.
+// tiles, so the token scales it reads for a group serve MMQ_TILES products. The K loop takes 256
+// weights a step: a Q6_K block, or 8 Q8_0 blocks per row. Each step the workgroup stages its
+// rows' step bytes (coalesced 16-byte loads, as the decode kernels do) and the 128 tokens' 256
+// int8 values (row stride padded against bank conflicts) and scales (group-major) in LDS, and
+// loads the next step's bytes into registers while this one is multiplied.
 //
 // In each MFMA the rows are N (lane l holds row l % 32 and, per lane half h = l / 32, 16 of the
 // group's 32 values), the tokens M (lane l holds token l % 32 of the token tile), and the result
@@ -17,6 +18,7 @@
 #include <algorithm>
 
 #include "blocks.h"
+#include "prefill.h"
 
 namespace leat {
 
@@ -76,7 +78,6 @@ __device__ __forceinline__ u32x4 lds_u4_even(uint32_t at) {
 // A step's weight bytes per row: 256 weights from the step's first byte rounded down to 4 (rows
 // start 4-byte aligned), as CPR chunks of 16 bytes, kept at a row stride of RS bytes.
 template <int TYPE> struct QGeo;
-template <> struct QGeo<Q4_K> { static constexpr int STEP_BYTES = 144, CPR = 9, RS = 176; };
 template <> struct QGeo<Q6_K> { static constexpr int STEP_BYTES = 210, CPR = 14, RS = 240; };
 template <> struct QGeo<Q8_0> { static constexpr int STEP_BYTES = 272, CPR = 17, RS = 304; };
 
@@ -182,41 +183,8 @@ __device__ __forceinline__ float x_scale(uint32_t off, int w, int g, int r, int 
     return h == 0 ? v : 0.0f;
 }
 
-// one step: acc[q] += the share of the lane's row in row tile q for the wave's token tile; Q4_K's
-// mins go to mins[q], kept apart so the matrix cores add them without waiting on the VALU
+// one step: acc[q] += the share of the lane's row in row tile q for the wave's token tile
 template <int TYPE> struct QCompute;
-
-template <>
-struct QCompute<Q4_K> {
-    __device__ static void run(int w, int r, int h, v16f (&acc)[MMQ_TILES], v16f (&mins)[MMQ_TILES]) {
-        u32x4 hdr[MMQ_TILES];
-#pragma unroll
-        for (int q = 0; q < MMQ_TILES; q++) hdr[q] = lds_u4(MMQ_W + (32 * q + r) * QGeo<Q4_K>::RS);
-        const v16f zero = {};
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const int j = g >> 1, e = g & 1;
-            const v4i x = x_operand(w, r, h, g);
-            const float xd = x_scale(MMQ_XD, w, g, r, h), xs = x_scale(MMQ_XS, w, g, r, h);
-#pragma unroll
-            for (int q = 0; q < MMQ_TILES; q++) {
-                const u32x4 qs = lds_u4(MMQ_W + (32 * q + r) * QGeo<Q4_K>::RS + 16 + 32 * j + 16 * h);
-                const u32x4 b = e ? ((qs >> 4) & 0x0F0F0F0Fu) : (qs & 0x0F0F0F0Fu);
-                // get_scale_min_k4 (leat/quant.py:182-187), g known at compile time
-                const uint32_t sh = 8u * (uint32_t)(g & 3);
-                const uint32_t x0 = hdr[q][1] >> sh, x1 = hdr[q][2] >> sh, x2 = hdr[q][3] >> sh;
-                const uint32_t scv = g < 4 ? (x0 & 63u) : ((x2 & 15u) | ((x0 >> 2) & 0x30u));
-                const uint32_t mv = g < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
-                const float sc = f16_lo(hdr[q][0]) * (float)scv, mn = f16_hi(hdr[q][0]) * (float)mv;
-                const v16i D = mmq_mfma(x, b);
-                const v16f S = outer(xd, h == 0 ? sc : 0.0f, zero);  // sc[row] * xd[token]
-                mins[q] = outer(xs, h == 0 ? -mn : 0.0f, mins[q]);    // - m[row] * xs[token]
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[q][v] += (float)D[v] * S[v];
-            }
-        }
-    }
-};
 
 template <>
 struct QCompute<Q6_K> {
@@ -298,16 +266,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const int tok0 = blockIdx.y * MMQ_TOKENS;
     const int steps = args.cols / MMQ_K;
     const int nb = args.cols / (TYPE == Q8_0 ? 32 : 256);
-    const int64_t row_bytes = (int64_t)nb * (TYPE == Q8_0 ? 34 : TYPE == Q4_K ? 144 : 210);
+    const int64_t row_bytes = (int64_t)nb * (TYPE == Q8_0 ? 34 : 210);
 
     WStage<TYPE> ws;
     XStage xs;
     wstage_load<TYPE, GATED>(ws, args, row_bytes, row0, 0, tid);
     xstage_load(xs, args, tok0, 0, tid);
 
-    v16f acc[MMQ_TILES], mins[MMQ_TILES];
+    v16f acc[MMQ_TILES];
 #pragma unroll
-    for (int q = 0; q < MMQ_TILES; q++) acc[q] = mins[q] = v16f{};
+    for (int q = 0; q < MMQ_TILES; q++) acc[q] = v16f{};
 
     for (int step = 0; step < steps; step++) {
         __syncthreads();  // every wave is done with the previous step's LDS
@@ -323,15 +291,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                 QCompute<Q6_K>::run<true>(step, wave, r, h, acc);
             else
                 QCompute<Q6_K>::run<false>(step, wave, r, h, acc);
-        } else if constexpr (TYPE == Q4_K) {
-            QCompute<Q4_K>::run(wave, r, h, acc, mins);
         } else {
             QCompute<Q8_0>::run(wave, r, h, acc);
         }
     }
-    if (TYPE == Q4_K)
-#pragma unroll
-        for (int q = 0; q < MMQ_TILES; q++) acc[q] += mins[q];
 
     // row tile q holds rows row0 + 32q (gated: the first half gate's, the second up's same rows)
     constexpr int OUT_TILES = GATED ? MMQ_TILES / 2 : MMQ_TILES;
@@ -364,7 +327,6 @@ static int mmq_launch(MmqArgs& a, hipStream_t st) {
 template <int MODE>
 static int mmq_dispatch(int type, MmqArgs& a, hipStream_t st) {
     switch (type) {
-    case Q4_K: return mmq_launch<Q4_K, MODE>(a, st);
     case Q6_K: return mmq_launch<Q6_K, MODE>(a, st);
     case Q8_0: return mmq_launch<Q8_0, MODE>(a, st);
     default: set_error("matmul: unsupported type %d", type); return -1;
@@ -382,6 +344,8 @@ static int mmq_check(int type, const void* w, int rows, int cols, const int32_t*
     const int64_t row_bytes = type == Q8_0 ? (int64_t)cols / 32 * 34 : (int64_t)cols / 256 * (type == Q4_K ? 144 : 210);
     LEAT_REQUIRE(row_bytes % 4 == 0, "matmul: rows of %lld bytes do not keep blocks 4-byte aligned", (long long)row_bytes);
     LEAT_REQUIRE((uintptr_t)w % 4 == 0 && (uintptr_t)xq % 16 == 0, "matmul: weights must be 4-byte and words 16-byte aligned");
+    // Q4_K's kernels load 16-byte chunks of its 144-byte blocks
+    LEAT_REQUIRE(type != Q4_K || (uintptr_t)w % 16 == 0, "matmul: Q4_K weights must be 16-byte aligned");
     return 0;
 }
 
@@ -392,6 +356,9 @@ using namespace leat;
 extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd,
                            const float* xs, int tokens, const float* residual, float* out, void* stream) {
     if (mmq_check(type, w, rows, cols, xq, xd, xs, tokens, out)) return -1;
+    if (type == Q4_K)
+        return prefill_launch(MMQ_RESIDUAL * (residual != nullptr), &w, rows, cols, xq, xd, xs, tokens, residual, 0, out,
+                              (hipStream_t)stream);
     MmqArgs a = {};
     a.w[0] = a.w[1] = (const uint8_t*)w;
     a.out = out;
@@ -407,6 +374,9 @@ extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int r
     if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, out) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, out))
         return -1;
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul: unknown GLU kind %d", kind);
+    const void* ws[2] = {gate, up};
+    if (type == Q4_K)
+        return prefill_launch(MMQ_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream);
     MmqArgs a = {};
     a.w[0] = (const uint8_t*)gate;
     a.w[1] = (const uint8_t*)up;
