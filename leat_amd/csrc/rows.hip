@@ -3,7 +3,9 @@
 //
 // Work split: lane l of a wave owns the same tasks of every row (tasks l, l + 64, ...; a task is
 // 32 weights of Q4_K or Q6_K, 64 of Q8_0, as in blocks.h), so it loads its activation words and
-// scales into registers once and reuses them for every row the wave streams. A wave owns RPW
+// scales into registers once and reuses them for every row the wave streams. Rows of 14336
+// weights (seven turns of a wave's tasks) are split by columns instead: each of 7 waves takes one
+// turn of the same few rows (rows_split_kernel). A wave owns RPW
 // consecutive rows (of each matrix of the launch: gate and up for the GLU) and walks them one at
 // a time, the loads of the next rows (up to 4) in flight while the current row is computed. A row's sum
 // is one wave-wide DPP reduction.
@@ -251,9 +253,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     for (int p = 0; p < P; p++)
         if (row0 + STEP * p < rows) fetch(buf[p], row0 + STEP * p);
 
-    // The activations: in registers, or for long rows (NT > 4) in LDS, read again for every row,
-    // with only RT::act's lane constants (Q6_K's offset sums) kept in registers
-    constexpr bool ACT_LDS = NT > 4;
+    // The activations, in registers
     if (XF32) {
         // the workgroup quantizes the tokens' rows into LDS: words, then d, then s
         const int words = B * (cols / 4), groups = B * (cols / GROUP);
@@ -266,21 +266,10 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
                                    lds_d + groups + t * (cols / GROUP));
         }
         __syncthreads();
-    } else if (ACT_LDS) {
-        // q8 input staged: words, then d, then s (Q4_K only)
-        const int words = B * (cols / 4), groups = B * (cols / GROUP);
-        for (int i = threadIdx.x; i < words / 4; i += WPG * 64)
-            ((u32x4*)rows_lds)[i] = ((const u32x4*)a.xq)[i];
-        float* lds_d = (float*)(rows_lds + words);
-        for (int i = threadIdx.x; i < groups; i += WPG * 64) {
-            lds_d[i] = a.xd[i];
-            if (TYPE == Q4_K) lds_d[groups + i] = a.xs[i];
-        }
-        __syncthreads();
     }
     auto fresh = [&](int i, int t, const uint32_t* lds) -> ActQ {
         const int task = has[i] ? lane + WAVE * i : 0;
-        return XF32 || ACT_LDS ? load_act_lds<TYPE>(lds, B, cols, t, task)
+        return XF32 ? load_act_lds<TYPE>(lds, B, cols, t, task)
                                : load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, task);
     };
     ActQ act[NT][B];
@@ -299,27 +288,13 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
         for (int k = 0; k < NM; k++)
 #pragma unroll
             for (int t = 0; t < B; t++) acc[k][t] = 0.0f;
-        // the LDS activations' base, opaque to the compiler so it reads them again for each row
-        // rather than holding all of them in registers
-        const uint32_t* lds_row = rows_lds;
-        if (ACT_LDS) asm volatile("" : "+v"(lds_row));
 #pragma unroll
         for (int i = 0; i < NT; i++) {
             if (!has[i]) continue;
 #pragma unroll
             for (int k = 0; k < NM; k++)
 #pragma unroll
-                for (int t = 0; t < B; t++) {
-                    ActQ x = act[i][t];
-                    if (ACT_LDS) {  // the words and scales again from LDS, the lane constants kept
-                        const ActQ again = fresh(i, t, lds_row);
-                        x.d0 = again.d0, x.d1 = again.d1;
-#pragma unroll
-                        for (int j = 0; j < 4; j++) x.x0[j] = again.x0[j], x.x1[j] = again.x1[j];
-                        if (TYPE == Q4_K) x.s0 = again.s0, x.s1 = again.s1;
-                    }
-                    acc[k][t] += RT::dot(buf[r % P][k][i], off, x);
-                }
+                for (int t = 0; t < B; t++) acc[k][t] += RT::dot(buf[r % P][k][i], off, act[i][t]);
         }
         // the slot is free again: the row P further on
         if (r + P < RPW && row + STEP * P < rows) fetch(buf[r % P], row + STEP * P);
@@ -371,6 +346,63 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
+#ifndef LEAT_ROWS_SPLIT_P
+#define LEAT_ROWS_SPLIT_P 2  // rows of loads a wave has in flight when long rows are split by columns
+#endif
+
+// Long rows (more than 4 turns of a wave's tasks: Q6_K or Q4_K rows of 14336 weights, 7 turns)
+// split by columns: wave w of the KS waves of a workgroup takes turn w of every row, tasks
+// 64w + lane, so each lane holds one task's activations and streams the workgroup's R rows with P
+// of them in flight; the waves' partial sums of a row meet in LDS and are added in wave order.
+template <int TYPE, int B, int KS, int R, int MODE>
+__global__ __launch_bounds__(KS * 64) void rows_split_kernel(RowsArgs a) {
+    using RT = RowTask<TYPE>;
+    constexpr int P = R < LEAT_ROWS_SPLIT_P ? R : LEAT_ROWS_SPLIT_P;
+    __shared__ float part[KS][B][R];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int cols = a.cols, rows = a.rows[0], row0 = blockIdx.x * R;
+    const uint32_t row_bytes = (uint32_t)(cols / Task<TYPE>::WEIGHTS) * Task<TYPE>::BYTES;
+    const int task = WAVE * w + lane;
+    const typename RT::Off off = RT::at(task);
+
+    typename RT::Raw buf[P];
+    auto fetch = [&](typename RT::Raw& dst, int row) {
+        dst = RT::load(a.w[0] + (size_t)min(row, rows - 1) * row_bytes, off);  // rows past the end: never stored
+    };
+#pragma unroll
+    for (int p = 0; p < P; p++) fetch(buf[p], row0 + p);
+    ActQ act[B];
+#pragma unroll
+    for (int t = 0; t < B; t++) act[t] = RT::act(load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, task), lane);
+
+    float sum[B][R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float acc[B];
+#pragma unroll
+        for (int t = 0; t < B; t++) acc[t] = RT::dot(buf[r % P], off, act[t]);
+        if (r + P < R) fetch(buf[r % P], row0 + r + P);
+#pragma unroll
+        for (int t = 0; t < B; t++) sum[t][r] = wave_sum_dpp(acc[t]);
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int t = 0; t < B; t++)
+#pragma unroll
+            for (int r = 0; r < R; r++) part[w][t][r] = sum[t][r];
+    __syncthreads();
+    if ((int)threadIdx.x < B * R) {
+        const int t = threadIdx.x / R, r = threadIdx.x % R, row = row0 + r;
+        float y = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KS; i++) y += part[i][t][r];
+        const int64_t at = (int64_t)t * rows + row;
+        if (MODE == ROWS_RESIDUAL) y += a.residual[at];
+        if (row < rows) a.out[0][at] = y;
+    }
+}
+
 // ------------------------------------------------------------------------------- launching
 
 template <int TYPE, int B, int NT, int RPW, int WPG, int MODE, bool XF32>
@@ -382,7 +414,7 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
         total += (a.rows[i] + WPG * RPW - 1) / (WPG * RPW);
     }
     a.tile_start[a.count] = total;
-    const size_t lds = XF32 || NT > 4 ? (size_t)B * a.cols + 2 * (size_t)B * (a.cols / GROUP) * 4 : 0;
+    const size_t lds = XF32 ? (size_t)B * a.cols + 2 * (size_t)B * (a.cols / GROUP) * 4 : 0;
     if (full)
         hipLaunchKernelGGL((rows_kernel<TYPE, B, NT, RPW, WPG, MODE, XF32, true>), dim3(total), dim3(WPG * 64), lds,
                            st, a);
@@ -398,11 +430,8 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
 #ifndef LEAT_ROWS_WPG
 #define LEAT_ROWS_WPG 8  // waves per workgroup in the plain and residual products
 #endif
-#ifndef LEAT_ROWS_LONG
-#define LEAT_ROWS_LONG 0  // take rows of more than 256 tasks (Q6_K 14336) on these kernels
-#endif
-#ifndef LEAT_ROWS_LONG_WPG
-#define LEAT_ROWS_LONG_WPG 4  // waves per workgroup for rows of more than 256 tasks (Q6_K 14336)
+#ifndef LEAT_ROWS_SPLIT_R
+#define LEAT_ROWS_SPLIT_R 2  // rows a workgroup streams when long rows are split by columns (more, fewer workgroups: slower)
 #endif
 #ifndef LEAT_ROWS_GLU_WPG
 #define LEAT_ROWS_GLU_WPG 8  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
@@ -410,9 +439,8 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
 
 template <int TYPE, int B, int NT, int MODE>
 static int rows_shape(RowsArgs& a, bool xf32, hipStream_t st) {
-    // long rows (seven tasks a lane) one row a wave: their loads alone fill the registers
-    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : NT > 4 ? LEAT_ROWS_LONG_WPG : LEAT_ROWS_WPG;
-    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : NT > 4 ? 1 : LEAT_ROWS_RPW;
+    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : LEAT_ROWS_WPG;
+    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : LEAT_ROWS_RPW;
     return xf32 ? rows_go<TYPE, B, NT, RPW, WPG, MODE, true>(a, st) : rows_go<TYPE, B, NT, RPW, WPG, MODE, false>(a, st);
 }
 
@@ -421,12 +449,24 @@ static int rows_nt(RowsArgs& a, bool xf32, hipStream_t st) {
     const int tasks = a.cols / Task<TYPE>::TASK_W;
     if (tasks <= WAVE) return rows_shape<TYPE, B, 1, MODE>(a, xf32, st);
     if (tasks <= 2 * WAVE) return rows_shape<TYPE, B, 2, MODE>(a, xf32, st);
-    if (tasks > 4 * WAVE) {  // Q6_K rows up to 14336 weights; not for the GLU (rows_fits)
-        if constexpr (MODE == ROWS_GLU) {
-            set_error("rows: GLU rows of %d tasks", tasks);
+    if (tasks > 4 * WAVE) {  // long rows, split by columns: one matrix, q8 input, no GLU (rows_fits)
+        if constexpr (MODE == ROWS_GLU || TYPE == Q8_0) {
+            set_error("rows: rows of %d tasks", tasks);
             return -1;
         } else {
-            return rows_shape<TYPE, B, 7, MODE>(a, xf32, st);
+            if (xf32 || tasks != 7 * WAVE) {
+                set_error("rows: long rows of %d tasks take quantized input, 7 turns", tasks);
+                return -1;
+            }
+            constexpr int R = LEAT_ROWS_SPLIT_R;
+            RowsArgs one = a;
+            for (int i = 0; i < a.count; i++) {  // a launch per matrix
+                one.w[0] = a.w[i], one.out[0] = a.out[i], one.rows[0] = a.rows[i];
+                hipLaunchKernelGGL((rows_split_kernel<TYPE, B, 7, R, MODE>), dim3((a.rows[i] + R - 1) / R), dim3(7 * WAVE),
+                                   0, st, one);
+                if (check_launch("rows")) return -1;
+            }
+            return 0;
         }
     }
     return rows_shape<TYPE, B, 4, MODE>(a, xf32, st);
@@ -442,13 +482,12 @@ bool rows_fits(int type, int cols, int tokens, bool glu) {
     return false;
 #endif
     if (tokens < 1 || tokens > ROWS_MAX_TOKENS) return false;
-    if (type == Q4_K) return cols % 256 == 0 && cols / 32 <= 4 * WAVE;
+    // rows of 7 turns of a wave's 32-weight tasks (14336 weights), split by columns: q8 input, no GLU
+    const bool split = !glu && cols == 7 * WAVE * 32;
+    if (type == Q4_K) return cols % 256 == 0 && (cols / 32 <= 4 * WAVE || split);
     if (type == Q8_0) return cols % 64 == 0 && cols / 64 <= 2 * WAVE;
-    // Q6_K rows of whole block pairs (4-byte aligned rows), up to 14336 weights; only with q8 input
-    // Q6_K rows of whole 512s: up to 8192 weights; longer ones (seven tasks a lane, supported below
-    // with the activations in LDS) measured slower than the v_dot4 kernel at 14336, so they stay off
-    // unless LEAT_ROWS_LONG is set
-    if (type == Q6_K) return cols % 512 == 0 && cols / 32 <= (glu || !LEAT_ROWS_LONG ? 4 : 7) * WAVE;
+    // Q6_K rows of whole 512s (block pairs: 4-byte aligned rows)
+    if (type == Q6_K) return cols % 512 == 0 && (cols / 32 <= 4 * WAVE || split);
     return false;
 }
 
@@ -477,7 +516,7 @@ using namespace leat;
 static int rows_f32_check(int type, int cols, const float* x, int tokens, bool glu) {
     if (check_cols(type, cols)) return -1;
     LEAT_REQUIRE(x, "null activations");
-    LEAT_REQUIRE(rows_fits(type, cols, tokens, glu),
+    LEAT_REQUIRE(rows_fits(type, cols, tokens, glu) && cols <= 8192,
                  "type %d, %d columns, %d tokens: the kernels that quantize their own input take Q4_K and Q8_0 rows "
                  "of at most 8192 weights, Q6_K rows of whole 512s up to 8192, and 1..%d tokens",
                  type, cols, tokens, ROWS_MAX_TOKENS);
