@@ -303,9 +303,10 @@ EXPERT_BYTES = 2 * nbytes(Q4_K, MOE_HIDDEN, MOE_DIM) + nbytes(Q6_K, MOE_DIM, MOE
 def measure_moe(torch, lib, B, steps, device, layers):
     """Config 5: the mixture of one token (B=1) or 8 streams (B=8) through 48 layers of 128
     experts (gate and up 768 x 2048 Q4_K, down 2048 x 768 Q6_K, top 8, router logits N(0,1)):
-    per layer route, norm+quantize, the chosen experts' gate+up+GLU, quantize, their down
-    (+residual), as leat's mixture on the matrix-vector kernels (leat/kernels/experts.py:
-    341-377). Weight bytes are each layer's distinct chosen experts, read once each."""
+    per layer route, norm+quantize, the chosen experts' gate+up+GLU, quantize (one launch,
+    leat_experts_glu_f32), their down (+residual), as leat's mixture on the matrix-vector
+    kernels (leat/kernels/experts.py:341-377). Weight bytes are each layer's distinct chosen
+    experts, read once each."""
     f32 = dict(dtype=torch.float32, device=device)
     i32 = dict(dtype=torch.int32, device=device)
     gen = torch.Generator(device=device).manual_seed(5)
@@ -314,24 +315,17 @@ def measure_moe(torch, lib, B, steps, device, layers):
     xs = [torch.randn(B, MOE_DIM, generator=gen, **f32) for _ in range(2)]
     norm_w = torch.rand(MOE_DIM, generator=gen, **f32) + 0.5
     ids, weights = torch.empty(P, **i32), torch.empty(P, **f32)
-    xq, xd, xs_ = torch.empty(B * MOE_DIM // 4, **i32), torch.empty(B * MOE_DIM // 32, **f32), torch.empty(B * MOE_DIM // 32, **f32)
-    h = torch.empty(P, MOE_HIDDEN, **f32)
     hq, hd, hs = torch.empty(P * MOE_HIDDEN // 4, **i32), torch.empty(P * MOE_HIDDEN // 32, **f32), torch.empty(P * MOE_HIDDEN // 32, **f32)
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     distinct = []
 
     def layer(i, w, which="all"):
         x, x_next = xs[i % 2], xs[(i + 1) % 2]
-        if which in ("all",):
-            _call(lib, "leat_route", scores[i].data_ptr(), B, MOE_EXPERTS, MOE_USED, ids.data_ptr(), weights.data_ptr(), st())
-            _call(lib, "leat_quantize_q8", x.data_ptr(), B, MOE_DIM, norm_w.data_ptr(), 1e-5, xq.data_ptr(),
-                  xd.data_ptr(), xs_.data_ptr(), st())  # fmt: skip
         if which in ("all", "glu"):
-            _call(lib, "leat_experts_glu", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), MOE_EXPERTS, MOE_HIDDEN,
-                  MOE_DIM, xq.data_ptr(), xd.data_ptr(), xs_.data_ptr(), ids.data_ptr(), P, MOE_USED, None, None, 0,
-                  h.data_ptr(), st())  # fmt: skip
-        if which in ("all",):
-            _call(lib, "leat_quantize_q8", h.data_ptr(), P, MOE_HIDDEN, None, 0.0, hq.data_ptr(), hd.data_ptr(),
+            # route, norm + quantize, the chosen experts' gate+up+GLU and its q8 output: one launch
+            _call(lib, "leat_experts_glu_f32", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), MOE_EXPERTS,
+                  MOE_HIDDEN, MOE_DIM, x.data_ptr(), B, norm_w.data_ptr(), 1e-5, scores[i].data_ptr(), MOE_USED,
+                  None, None, 0, ids.data_ptr(), weights.data_ptr(), None, hq.data_ptr(), hd.data_ptr(),
                   hs.data_ptr(), st())  # fmt: skip
         if which in ("all", "down"):
             _call(lib, "leat_experts_down", Q6_K, w["down"].data_ptr(), MOE_EXPERTS, MOE_DIM, MOE_HIDDEN,
@@ -348,7 +342,9 @@ def measure_moe(torch, lib, B, steps, device, layers):
     down_us = _graph_us(torch, lambda: [layer(i, w, "down") for i, w in enumerate(layers)], steps) / MOE_LAYERS
     last = distinct[-1]
     step_bytes = sum(distinct) * EXPERT_BYTES
-    glu_bytes = last * 2 * nbytes(Q4_K, MOE_HIDDEN, MOE_DIM) + B * (MOE_DIM + MOE_DIM // 32 * 8) + P * MOE_HIDDEN * 4
+    # the chosen experts' gate and up, the f32 input and scores, the q8 hidden rows written
+    glu_bytes = (last * 2 * nbytes(Q4_K, MOE_HIDDEN, MOE_DIM) + B * (MOE_DIM + MOE_EXPERTS) * 4
+                 + P * (MOE_HIDDEN + MOE_HIDDEN // 32 * 8))  # fmt: skip
     gbs = step_bytes / (step_us * 1e-6) / 1e9
     glu_gbs = glu_bytes / (glu_us * 1e-6) / 1e9
     return {

@@ -138,6 +138,21 @@ int leat_experts_glu(int type, const void *gate, const void *up, int experts, in
                      int used, const float *gate_bias, const float *up_bias, int kind, float *out,
                      void *stream);
 
+/* Replaces the first four steps of a decode mixture, leat/kernels/experts.py:341-359 (route,
+ * quantize_q8 of rms_norm(x), experts_swiglu) and the quantize_q8 of its hidden rows that
+ * leat_experts_down consumes, in one launch: routes `tokens` (1..8) rows of scores (tokens,
+ * experts) f32 as leat_route (writing ids and weights, tokens * used), quantizes x (tokens, cols)
+ * f32 after RMSNorm with norm_weight and eps (NULL: none) as leat_quantize_q8, and computes
+ * out[p * rows + r] as leat_experts_glu; out may be NULL. hq, hd, hs receive leat_quantize_q8 of
+ * those pairs * rows values (rows a multiple of 32). Limits: experts <= 256, used <= 64; rows of
+ * Q4_K (cols a multiple of 256), Q6_K (of 512) or Q8_0 (of 64) of at most 8192 weights; x and
+ * norm_weight 16-byte aligned. An expert chosen by more than 2 tokens is read once per 2 of them. */
+int leat_experts_glu_f32(int type, const void *gate, const void *up, int experts, int rows, int cols,
+                         const float *x, int tokens, const float *norm_weight, float eps,
+                         const float *scores, int used, const float *gate_bias, const float *up_bias,
+                         int kind, int32_t *ids, float *weights, float *out, int32_t *hq, float *hd,
+                         float *hs, void *stream);
+
 /* Replaces the down kernel of leat/kernels/experts.py:360-371 (_experts_down_kernel, :241-270):
  * out[t * rows + r] = sum over slots s < used of weights[p] * scales[e] * (w[e] row r . h[p]
  * + bias[e * rows + r]) (+ residual[t * rows + r]), p = t * used + s, e = ids[p]; h the pairs'

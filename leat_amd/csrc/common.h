@@ -96,6 +96,34 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// the same reduction for max (floats) and min (ints): lanes a move leaves out keep the operation's
+// identity (-inf, INT_MAX) as their moved value
+#define LEAT_DPP_ID(id, v, ctrl, rm, bm) __builtin_amdgcn_update_dpp(id, v, ctrl, rm, bm, false)
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    const int ninf = __builtin_bit_cast(int, -INFINITY);
+#define LEAT_MAX_STEP(ctrl, rm, bm) \
+    v = fmaxf(v, __builtin_bit_cast(float, LEAT_DPP_ID(ninf, __builtin_bit_cast(int, v), ctrl, rm, bm)))
+    LEAT_MAX_STEP(0xB1, 0xF, 0xF);
+    LEAT_MAX_STEP(0x4E, 0xF, 0xF);
+    LEAT_MAX_STEP(0x114, 0xF, 0xE);
+    LEAT_MAX_STEP(0x118, 0xF, 0xC);
+    LEAT_MAX_STEP(0x142, 0xA, 0xF);
+    LEAT_MAX_STEP(0x143, 0xC, 0xF);
+#undef LEAT_MAX_STEP
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ int wave_min_dpp(int v) {
+#define LEAT_MIN_STEP(ctrl, rm, bm) v = min(v, LEAT_DPP_ID(0x7FFFFFFF, v, ctrl, rm, bm))
+    LEAT_MIN_STEP(0xB1, 0xF, 0xF);
+    LEAT_MIN_STEP(0x4E, 0xF, 0xF);
+    LEAT_MIN_STEP(0x114, 0xF, 0xE);
+    LEAT_MIN_STEP(0x118, 0xF, 0xC);
+    LEAT_MIN_STEP(0x142, 0xA, 0xF);
+    LEAT_MIN_STEP(0x143, 0xC, 0xF);
+#undef LEAT_MIN_STEP
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WAVE));

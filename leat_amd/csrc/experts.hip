@@ -15,6 +15,8 @@
 #include <cfloat>
 
 #include "blocks.h"
+#include "q8.h"
+#include "rowtask.h"
 
 namespace leat {
 
@@ -22,18 +24,17 @@ constexpr float LOG2E = 1.4426950408889634f;
 
 // ------------------------------------------------------------------------------------- route
 
-// EPL experts per lane: experts <= 64 EPL
+// Routes one token's scores (experts <= 64 EPL, used <= 64) on one wave: `used` rounds of wave
+// argmax (ties to the lower id; -inf and NaN count as the least finite score, below which a taken
+// winner drops), then the softmax of the winners. Lane r < used gets round r's winner and weight.
 template <int EPL>
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ scores, int tokens, int experts,
-                                                    int used, int32_t* __restrict__ ids, float* __restrict__ weights) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
-    if (t >= tokens) return;
+__device__ __forceinline__ void route_token(const float* __restrict__ row, int experts, int used, int lane, int* id,
+                                            float* weight) {
     float v[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = lane + WAVE * i;
-        const float s = e < experts ? scores[(int64_t)t * experts + e] : -INFINITY;
+        const float s = e < experts ? row[e] : -INFINITY;
         // -inf and NaN as the least finite value; lanes past the experts below every score
         v[i] = e < experts ? (s > -FLT_MAX ? s : -FLT_MAX) : -INFINITY;
     }
@@ -45,26 +46,38 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ sc
 #pragma unroll
         for (int i = 1; i < EPL; i++)  // ascending ids: strictly greater keeps the lower on ties
             if (v[i] > best) best = v[i], index = lane + WAVE * i;
-#pragma unroll
-        for (int off = WAVE / 2; off > 0; off >>= 1) {
-            const float ob = __shfl_xor(best, off);
-            const int oi = __shfl_xor(index, off);
-            if (ob > best || (ob == best && oi < index)) best = ob, index = oi;
-        }
+        // the wave's maximum, then the lowest id holding it: two DPP reductions (no LDS round
+        // trips); a taken winner (-inf) never ties an untaken score (at least -FLT_MAX)
+        const float top = wave_max_dpp(best);
+        const int winner = wave_min_dpp(best == top ? index : 0x7FFFFFFF);
 #pragma unroll
         for (int i = 0; i < EPL; i++)
-            if (lane + WAVE * i == index) v[i] = -INFINITY;  // taken: below every remaining score
-        if (lane == round) my_top = best, my_id = index;
+            if (lane + WAVE * i == winner) v[i] = -INFINITY;  // taken: below every remaining score
+        if (lane == round) my_top = top, my_id = winner;
     }
     // softmax of the winners, relative to the first (largest): exp2((top - top0) * log2 e), summed
     // in rounds' order (leat/kernels/experts.py:154-159)
-    const float top0 = __shfl(my_top, 0);
+    const float top0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_top), 0));
     const float e = lane < used ? exp2f((my_top - top0) * LOG2E) : 0.0f;
-    float total = __shfl(e, 0);
-    for (int r = 1; r < used; r++) total += __shfl(e, r);
+    float total = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), 0));
+    for (int r = 1; r < used; r++) total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
+    *id = my_id;
+    *weight = e / total;
+}
+
+// a wave per token
+template <int EPL>
+__global__ __launch_bounds__(256) void route_kernel(const float* scores, int tokens, int experts, int used,
+                                                    int32_t* __restrict__ ids, float* __restrict__ weights) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
+    if (t >= tokens) return;
+    int id;
+    float weight;
+    route_token<EPL>(scores + (int64_t)t * experts, experts, used, lane, &id, &weight);
     if (lane < used) {
-        ids[(int64_t)t * used + lane] = my_id;
-        weights[(int64_t)t * used + lane] = e / total;
+        ids[(int64_t)t * used + lane] = id;
+        weights[(int64_t)t * used + lane] = weight;
     }
 }
 
@@ -163,6 +176,230 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
             if (j >= n) m[j] = m[0];
         glu_rows<TYPE, C>(a, e, row, m, n, lane);
     }
+}
+
+// ------------------------------------------------------------------ fused decode GLU (1..8 tokens)
+
+// The first steps of a decode mixture in one launch (leat/kernels/experts.py:341-377: route,
+// quantize_q8 of rms_norm(x), experts_swiglu, quantize_q8 of the hidden rows). A workgroup owns
+// 32 rows of the expert of pair p = blockIdx.y:
+// 1. its 8 waves route every token (route_token, the routing kernel's arithmetic) into LDS, and
+//    workgroup (0, 0) publishes ids and weights for the down product;
+// 2. the pairs routed to one expert (at most one a token) are served C at a time, by the
+//    workgroups of the first, (C+1)-th, ... of them; the others exit. With C = 2 slots an expert
+//    is read once unless more than 2 tokens chose it;
+// 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
+//    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes the
+//    member tokens' x into LDS with the standalone quantizer's arithmetic (q8.h);
+// 4. each wave streams 4 rows of gate and up against the members' activations in registers;
+// 5. the 32 rows are one group of 32 per pair, so the workgroup writes the hidden rows' q8 words,
+//    d and s as well as (optionally) their f32 values.
+#ifndef LEAT_MOE_WAVES
+#define LEAT_MOE_WAVES 8  // waves of a workgroup: 32 rows, 32 / LEAT_MOE_WAVES a wave (16 spill)
+#endif
+constexpr int MOE_WAVES = LEAT_MOE_WAVES, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
+
+struct MoeGluArgs {
+    const uint8_t* gate;
+    const uint8_t* up;
+    int64_t stride;  // rows per expert in the gate (and up) storage: 2 rows when gate stacks both
+    int up_first;    // the first up row within an expert's rows: rows when stacked, else 0
+    int experts, rows, cols, used, tokens;
+    const float* x;  // tokens * cols
+    const float* norm;
+    float eps;
+    const float* scores;  // tokens * experts
+    const float* gate_bias;
+    const float* up_bias;
+    int kind;
+    int32_t* ids;  // tokens * used, written
+    float* weights;
+    float* out;  // pairs * rows, or null
+    uint32_t* hq;
+    float* hd;
+    float* hs;
+};
+
+template <int TYPE, int NT, int C, int EPL>
+__global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
+    using RT = RowTask<TYPE>;
+    constexpr int RPW = MOE_TILE / MOE_WAVES;
+    constexpr int P = NT == 1 ? RPW : NT == 2 ? 2 : 1;  // rows of loads in flight
+    static_assert(NT * C <= 8, "members' activations in registers");
+    extern __shared__ uint32_t moe_lds[];  // the C member tokens' q8 rows: words, then d, then s
+    __shared__ int route_id[MOE_MAX_TOKENS * MOE_MAX_USED];
+    __shared__ float route_w[MOE_MAX_TOKENS * MOE_MAX_USED];
+    __shared__ float partial[MOE_WAVES];
+    __shared__ float glu_out[C][MOE_TILE];
+
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int p = blockIdx.y, row_base = blockIdx.x * MOE_TILE;
+    const int cols = a.cols, used = a.used, pairs = a.tokens * used;
+
+    // 1. routing
+    for (int t = w; t < a.tokens; t += MOE_WAVES) {
+        int id;
+        float weight;
+        route_token<EPL>(a.scores + (int64_t)t * a.experts, a.experts, used, lane, &id, &weight);
+        if (lane < used) route_id[t * used + lane] = id, route_w[t * used + lane] = weight;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && p == 0)
+        for (int i = threadIdx.x; i < pairs; i += MOE_WAVES * 64) a.ids[i] = route_id[i], a.weights[i] = route_w[i];
+
+    // 2. the expert of pair p, and its members (the same in every thread: LDS reads)
+    const int e = route_id[p];  // route_token ids are always below `experts`
+    int rank = 0;  // the pairs before p routed to e
+    for (int q = 0; q < p; q++) rank += route_id[q] == e;
+    if (rank % C != 0) return;  // the whole workgroup: an earlier pair's workgroup serves p
+    int m[C], n = 0;  // p and the next C - 1 pairs routed to e (at most one a token)
+#pragma unroll
+    for (int j = 0; j < C; j++) m[j] = p;
+    for (int q = p; q < pairs && n < C; q++)
+        if (route_id[q] == e) {
+#pragma unroll
+            for (int j = 0; j < C; j++)  // m[n] = q without indexing registers at run time
+                if (j == n) m[j] = q;
+            n++;
+        }
+
+    // 3. the rows' loads, then the members' activations
+    const int row0 = row_base + w;  // the wave's rows: row0 + 8r
+    const uint32_t row_bytes = (uint32_t)(cols / Task<TYPE>::WEIGHTS) * Task<TYPE>::BYTES;
+    const typename RT::Off off = RT::at(lane);
+    const int tasks = cols / Task<TYPE>::TASK_W;
+    bool has[NT];  // the lane's task i lies in the row (a last partial turn leaves lanes idle)
+#pragma unroll
+    for (int i = 0; i < NT; i++) has[i] = lane + WAVE * i < tasks;
+    const uint8_t* g_at = a.gate + (size_t)(e * a.stride) * row_bytes;
+    const uint8_t* u_at = a.up + (size_t)(e * a.stride + a.up_first) * row_bytes;
+    typename RT::Raw rg[P][NT], ru[P][NT];
+    auto fetch = [&](int slot, int r) {
+        const uint32_t at = (uint32_t)min(row0 + MOE_WAVES * r, a.rows - 1) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+            if (has[i]) {
+                rg[slot][i] = RT::load(g_at + at + RT::STRIDE * i, off);
+                ru[slot][i] = RT::load(u_at + at + RT::STRIDE * i, off);
+            }
+    };
+#pragma unroll
+    for (int r = 0; r < P; r++) fetch(r, r);
+    const int words = C * (cols / 4), groups = C * (cols / GROUP);
+    float* lds_d = (float*)(moe_lds + words);
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        if (j >= n) break;  // uniform
+        const float* xr = a.x + (int64_t)(m[j] / used) * cols;
+        const float inv = a.norm ? block_inv_rms<MOE_WAVES * 64>(xr, cols, a.eps, partial) : 1.0f;
+        quantize_row<MOE_WAVES * 64>(xr, cols, a.norm, inv, moe_lds + j * (cols / 4), lds_d + j * (cols / GROUP),
+                                     lds_d + groups + j * (cols / GROUP));
+    }
+    __syncthreads();
+    ActQ act[NT][C];
+#pragma unroll
+    for (int i = 0; i < NT; i++)
+#pragma unroll
+        for (int j = 0; j < C; j++)
+            act[i][j] = RT::act(load_act_lds<TYPE>(moe_lds, C, cols, j < n ? j : 0, has[i] ? lane + WAVE * i : 0), lane);
+
+    // 4. the rows
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const int row = row0 + MOE_WAVES * r;
+        float g[C], u[C];
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            g[j] = u[j] = 0.0f;
+            if (j >= n) continue;  // uniform: the expert serves n of the C slots
+#pragma unroll
+            for (int i = 0; i < NT; i++)
+                if (has[i]) {
+                    g[j] += RT::dot(rg[r % P][i], off, act[i][j]);
+                    u[j] += RT::dot(ru[r % P][i], off, act[i][j]);
+                }
+        }
+        if (r + P < RPW) fetch(r % P, r + P);
+        const float gb = a.gate_bias && row < a.rows ? a.gate_bias[(int64_t)e * a.rows + row] : 0.0f;
+        const float ub = a.up_bias && row < a.rows ? a.up_bias[(int64_t)e * a.rows + row] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            if (j >= n) break;  // uniform
+            const float y = glu(a.kind, wave_sum_dpp(g[j]) + gb, wave_sum_dpp(u[j]) + ub);
+            if (lane == 0) {
+                glu_out[j][w + MOE_WAVES * r] = y;
+                if (a.out && row < a.rows) a.out[(int64_t)m[j] * a.rows + row] = y;
+            }
+        }
+    }
+
+    // 5. each member's 32 outputs quantized as one group (rows a multiple of 32)
+    if (!a.hq) return;
+    __syncthreads();
+    if ((int)threadIdx.x < MOE_TILE * C) {
+        const int j = threadIdx.x / MOE_TILE, i = threadIdx.x % MOE_TILE;
+        int mj = m[0];
+#pragma unroll
+        for (int k = 1; k < C; k++)
+            if (k == j) mj = m[k];
+        const float v = glu_out[j][i];
+        float amax = fabsf(v);
+#pragma unroll
+        for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
+        const float scale = amax / 127.0f;
+        const int q = scale > 0.0f ? (int)roundf(v / scale) : 0;
+        int total = q;
+#pragma unroll
+        for (int sft = 1; sft < 32; sft <<= 1) total += __shfl_xor(total, sft, 32);
+        const uint32_t b0 = (uint32_t)(q & 0xFF);
+        const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
+        const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
+        const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
+        if (j < n) {
+            const int64_t first = (int64_t)mj * a.rows + row_base;
+            if ((i & 3) == 0) a.hq[(first + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (i == 0) {
+                a.hd[first / GROUP] = scale;
+                a.hs[first / GROUP] = scale * (float)total;
+            }
+        }
+    }
+}
+
+template <int TYPE, int NT, int C>
+static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
+    const dim3 grid((a.rows + MOE_TILE - 1) / MOE_TILE, a.tokens * a.used);
+    const size_t lds = (size_t)C * a.cols + 2 * (size_t)C * (a.cols / GROUP) * 4;
+    if (a.experts <= WAVE)
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 1>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+    else if (a.experts <= 2 * WAVE)
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 2>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+    else
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 4>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+}
+
+// turns * token slots the members' activations may take in registers: Q6_K and Q8_0 blocks
+// decode into more registers than Q4_K's, so their rows of several turns take fewer tokens
+__host__ __device__ constexpr int moe_budget(int type, int turns) {
+    return type == Q4_K || (type == Q6_K && turns == 1) ? 8 : 4;
+}
+
+// member slots a pass: 2 (an expert rarely serves more tokens; the rest in further passes) where
+// they fit the registers, else 1
+template <int TYPE, int NT>
+static void moe_glu_c(MoeGluArgs& a, hipStream_t st) {
+    if constexpr (2 * NT <= moe_budget(TYPE, NT))
+        if (a.tokens > 1) return moe_glu_go<TYPE, NT, 2>(a, st);
+    return moe_glu_go<TYPE, NT, 1>(a, st);
+}
+
+template <int TYPE>
+static void moe_glu_nt(MoeGluArgs& a, hipStream_t st) {
+    const int turns = a.cols / Task<TYPE>::TASK_W / WAVE;
+    if (turns <= 1) return moe_glu_c<TYPE, 1>(a, st);
+    if (turns <= 2) return moe_glu_c<TYPE, 2>(a, st);
+    return moe_glu_c<TYPE, 4>(a, st);
 }
 
 // ------------------------------------------------------------------------------- experts_down
@@ -282,4 +519,46 @@ extern "C" int leat_experts_down(int type, const void* w, int experts, int rows,
     case Q8_0: hipLaunchKernelGGL(experts_down_kernel<Q8_0>, grid, dim3(256), 0, st, a); break;
     }
     return check_launch("experts_down");
+}
+
+extern "C" int leat_experts_glu_f32(int type, const void* gate, const void* up, int experts, int rows, int cols,
+                                    const float* x, int tokens, const float* norm_weight, float eps,
+                                    const float* scores, int used, const float* gate_bias, const float* up_bias,
+                                    int kind, int32_t* ids, float* weights, float* out, int32_t* hq, float* hd,
+                                    float* hs, void* stream) {
+    LEAT_REQUIRE(gate && x && scores && ids && weights, "experts_glu_f32: null pointer");
+    LEAT_REQUIRE(out || hq, "experts_glu_f32: neither f32 nor q8 output");
+    LEAT_REQUIRE(tokens >= 1 && tokens <= MOE_MAX_TOKENS, "experts_glu_f32: %d tokens (1..%d)", tokens, MOE_MAX_TOKENS);
+    LEAT_REQUIRE(experts > 0 && experts <= 4 * WAVE, "experts_glu_f32: %d experts (1..256 supported)", experts);
+    LEAT_REQUIRE(used > 0 && used <= experts && used <= MOE_MAX_USED, "experts_glu_f32: %d of %d experts", used, experts);
+    LEAT_REQUIRE(rows > 0 && rows % MOE_TILE == 0, "experts_glu_f32: rows %d not a multiple of %d", rows, MOE_TILE);
+    LEAT_REQUIRE(!hq || (hd && hs), "experts_glu_f32: a q8 output needs d and s");
+    LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "experts_glu_f32: unknown GLU kind %d", kind);
+    // the row-streaming tasks: whole wave turns up to 4 (Q4_K rows of 256s, Q6_K of 512s: 4-byte
+    // aligned rows), 16-byte aligned f32 rows
+    const int tasks = type == Q8_0 ? cols / 64 : cols / 32;
+    LEAT_REQUIRE((type == Q4_K && cols % 256 == 0) || (type == Q6_K && cols % 512 == 0) || (type == Q8_0 && cols % 64 == 0),
+                 "experts_glu_f32: type %d, %d columns", type, cols);
+    LEAT_REQUIRE(tasks <= 4 * WAVE, "experts_glu_f32: rows of %d weights (at most 4 turns of a wave's tasks)", cols);
+
+    LEAT_REQUIRE((uintptr_t)x % 16 == 0 && (!norm_weight || (uintptr_t)norm_weight % 16 == 0),
+                 "experts_glu_f32: f32 rows must be 16-byte aligned");
+    if (check_ptrs(type, gate, nullptr) || (up && check_ptrs(type, up, nullptr))) return -1;
+    MoeGluArgs a = {};
+    a.gate = (const uint8_t*)gate;
+    a.up = (const uint8_t*)(up ? up : gate);
+    a.stride = up ? rows : 2 * (int64_t)rows;
+    a.up_first = up ? 0 : rows;
+    a.experts = experts, a.rows = rows, a.cols = cols, a.used = used, a.tokens = tokens;
+    a.x = x, a.norm = norm_weight, a.eps = eps, a.scores = scores;
+    a.gate_bias = gate_bias, a.up_bias = up_bias, a.kind = kind;
+    a.ids = ids, a.weights = weights, a.out = out;
+    a.hq = (uint32_t*)hq, a.hd = hd, a.hs = hs;
+    hipStream_t st = (hipStream_t)stream;
+    switch (type) {
+    case Q4_K: moe_glu_nt<Q4_K>(a, st); break;
+    case Q6_K: moe_glu_nt<Q6_K>(a, st); break;
+    case Q8_0: moe_glu_nt<Q8_0>(a, st); break;
+    }
+    return check_launch("experts_glu_f32");
 }
