@@ -27,6 +27,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -208,11 +209,26 @@ def measure(torch, lib, layers, B, steps, warmup, device):
         "tok_s": B * 1000.0 / ms,
         "glu_us": glu_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(GLU_KERNELS.get(B, "")),
+                     "traffic_source": "profiles/decode_linear_hbm_bytes.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)",
                      "kernel": f"gate+up GLU matvec, Q4_K 2x14336x4096, B={B}"
                                + (" (quantizes its f32 input and its output)" if B <= 2 else ""),
                      "bytes_per_launch": glu_bytes(B)},  # fmt: skip
     }
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_linear_hbm_bytes.md")
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per dispatch of `kernel` as the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    records them (calibrated against a copy of known size), or None if it does not."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^" + re.escape(kernel) + r" (\d+)$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def _graph_us(torch, fn, reps, inner=1):
@@ -232,6 +248,9 @@ def _graph_us(torch, fn, reps, inner=1):
     torch.cuda.synchronize()
     return 1000 * start.elapsed_time(end) / (reps * inner)
 
+
+# the GLU kernels of the decode legs, as rocprofv3 names them
+GLU_KERNELS = {1: "rows_kernel<12, 1, 2, 4, 8, 2, true, true>", 8: "tiles_kernel<12, 2, 4>"}
 
 PREFILL_TOKENS = 512
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
