@@ -110,9 +110,11 @@ class Step:
                   self.h.data_ptr(), B, self.norm_w.data_ptr(), 1e-5, 0, None, gq.data_ptr(), gd.data_ptr(),
                   gs.data_ptr(), st)  # fmt: skip
         else:
+            # q8 input; the f32 outputs and their q8 (the down product's input) from the same kernel
             xq, xd, xs = self.q8[HIDDEN]
-            _call(self.lib, "leat_glu_matvec", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
-                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), st)  # fmt: skip
+            _call(self.lib, "leat_glu_matvec_q8", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN,
+                  xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), B, 0, self.g.data_ptr(), gq.data_ptr(), gd.data_ptr(),
+                  gs.data_ptr(), st)  # fmt: skip
 
     def run_glu_only(self):
         for w in self.layers:
@@ -148,7 +150,6 @@ class Step:
                       as_.data_ptr(), B, x.data_ptr(), self.h.data_ptr(), st)  # fmt: skip
                 self.quantize(self.h, HIDDEN, self.q8[HIDDEN], True)
                 self.glu(w)
-                self.quantize(self.g, FFN, self.q8[FFN], False)
             _call(lib, "leat_matvec", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, gq.data_ptr(), gd.data_ptr(),
                   gs.data_ptr(), B, self.h.data_ptr(), x_next.data_ptr(), st)  # fmt: skip
 
@@ -161,11 +162,11 @@ def _call(lib, name, *args):
 def glu_bytes(B):
     # algorithmic bytes of one gate+up GLU launch: both matrices, then for one or two tokens the
     # f32 input read (and quantized in the kernel) and the q8 output written (int8 + d + s); for
-    # more tokens q8 input and f32 output
+    # more tokens q8 input, and f32 and q8 outputs
     weights = 2 * nbytes(Q4_K, FFN, HIDDEN)
     if B <= 2:
         return weights + B * HIDDEN * 4 + B * (FFN + FFN // 32 * 8)
-    return weights + B * (HIDDEN + HIDDEN // 32 * 8) + B * FFN * 4
+    return weights + B * (HIDDEN + HIDDEN // 32 * 8) + B * FFN * 4 + B * (FFN + FFN // 32 * 8)
 
 
 def measure(torch, lib, layers, B, steps, warmup, device):

@@ -60,6 +60,15 @@ int leat_glu_matvec(int type, const void *gate, const void *up, int rows, int co
                     const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
                     float *out, void *stream);
 
+/* leat_glu_matvec that also writes leat_quantize_q8 of its outputs, (tokens, rows) as
+ * (tokens * rows / 4) words and (tokens * rows / 32) scales and sums: the down product's input, as
+ * leat's feed_forward quantizes it (leat/ops.py:41-55). rows a multiple of 32. For 1..2 tokens and
+ * for 3..8 tokens of 16-byte aligned Q4_K the GLU kernel writes them itself; otherwise a quantize
+ * launch follows it. out is required. */
+int leat_glu_matvec_q8(int type, const void *gate, const void *up, int rows, int cols,
+                       const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
+                       float *out, int32_t *hq, float *hd, float *hs, void *stream);
+
 /* Replaces the whole of leat/kernels/matvec.py:362-380 matvecs(x, *ws, norm) for one or two
  * tokens: quantize_q8 of x (after RMSNorm with norm_weight and eps when norm_weight is not NULL)
  * and the products, in one launch. Each workgroup quantizes x itself with leat_quantize_q8's

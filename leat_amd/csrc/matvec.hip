@@ -8,6 +8,7 @@
 // the wave then sums its lanes and lane 0 stores. Several matrices that share the activations
 // (q, k and v) run in one launch: waves are numbered across them.
 #include "blocks.h"
+#include "leatmi.h"
 #include "mmv.h"
 #include "rows.h"
 #include "tiles.h"
@@ -28,6 +29,9 @@ struct MatvecArgs {
     const float* xs;
     const float* residual;  // MODE_RESIDUAL: tokens * rows[0]
     int kind;               // MODE_GLU: the GLU kind; w[0] gate, w[1] up, out[0]
+    uint32_t* hq;           // MODE_GLU: q8 of the outputs, where the kernel writes it (glu_q8_inside)
+    float* hd;
+    float* hs;
 };
 
 enum Mode : int { MODE_PLAIN = 0, MODE_RESIDUAL = 1, MODE_GLU = 2 };
@@ -215,6 +219,7 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         r.xq = a.xq, r.xd = a.xd, r.xs = a.xs;
         r.residual = a.residual;
         r.kind = a.kind;
+        r.hq = a.hq, r.hd = a.hd, r.hs = a.hs;
         return rows_launch(type, MODE, r, tokens, false, s);
     }
     if (LEAT_TILES && tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
@@ -230,6 +235,7 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         t.xq = a.xq, t.xd = a.xd, t.xs = a.xs;
         t.residual = a.residual;
         t.kind = a.kind;
+        t.hq = a.hq, t.hd = a.hd, t.hs = a.hs;
         return tiles_launch(type, MODE, t, s);
     }
     if (tokens >= LEAT_MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
@@ -317,6 +323,38 @@ extern "C" int leat_matvec(int type, const void* w, int rows, int cols, const in
     a.residual = residual;
     return residual ? dispatch<MODE_RESIDUAL>(type, a, tokens, (hipStream_t)stream)
                     : dispatch<MODE_PLAIN>(type, a, tokens, (hipStream_t)stream);
+}
+
+// whether dispatch<MODE_GLU> takes a kernel that writes the q8 of its outputs itself (rows a
+// multiple of 32): the row-streaming kernels (1..2 tokens) and the tile kernels (3..8 of Q4_K)
+static bool glu_q8_inside(int type, int cols, int tokens, const void* gate, const void* up) {
+    const void* ws[2] = {gate, up};
+    return rows_fits(type, cols, tokens, true) || (LEAT_TILES && tiles_fits(type, cols, tokens, ws, 2));
+}
+
+extern "C" int leat_glu_matvec_q8(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
+                                  const float* xd, const float* xs, int tokens, int kind, float* out, int32_t* hq,
+                                  float* hd, float* hs, void* stream) {
+    if (check_cols(type, cols)) return -1;
+    LEAT_REQUIRE(gate && up && out && xq && xd && xs && hq && hd && hs && rows > 0,
+                 "glu_matvec_q8: null pointer or empty matrix");
+    LEAT_REQUIRE(rows % GROUP == 0, "glu_matvec_q8: rows %d not a multiple of 32", rows);
+    LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matvec_q8: unknown GLU kind %d", kind);
+    if (check_ptrs(type, gate, xq) || check_ptrs(type, up, xq)) return -1;
+    MatvecArgs a = {};
+    a.w[0] = (const uint8_t*)gate;
+    a.w[1] = (const uint8_t*)up;
+    a.out[0] = out;
+    a.rows[0] = rows;
+    a.count = 1;
+    a.cols = cols;
+    a.xq = xq, a.xd = xd, a.xs = xs;
+    a.kind = kind;
+    const bool inside = glu_q8_inside(type, cols, tokens, gate, up);
+    if (inside) a.hq = (uint32_t*)hq, a.hd = hd, a.hs = hs;
+    if (dispatch<MODE_GLU>(type, a, tokens, (hipStream_t)stream)) return -1;
+    // other kernels: the outputs quantized by a second launch
+    return inside ? 0 : leat_quantize_q8(out, tokens, rows, nullptr, 0.0f, hq, hd, hs, stream);
 }
 
 extern "C" int leat_glu_matvec(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
