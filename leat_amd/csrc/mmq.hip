@@ -2,7 +2,8 @@
 // MMQ): out[t, r] = W[r] . x[t] for many tokens, the activations quantized to int8 per group of 32
 // as for decode, int32 products per group on v_mfma_i32_32x32x32_i8, scaled into f32 per group
 // exactly as leat's _Q6KTile / _Q80Tile.scaled (leat/kernels/matmul.py:379-387, 447-452). Q4_K
-// takes prefill.hip's kernels.
+// takes prefill.hip's kernels and the plain and residual Q6_K products prefill6.hip's; the Q6_K
+// gated product and Q8_0 stay here.
 //
 // A workgroup owns a tile of 128 tokens by MMQ_TILES row tiles of 32 (of one matrix, or half of
 // gate and the same rows of up); each of its 4 waves owns one 32-token tile for all the row
@@ -359,6 +360,8 @@ extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const in
     if (type == Q4_K)
         return prefill_launch(MMQ_RESIDUAL * (residual != nullptr), &w, rows, cols, xq, xd, xs, tokens, residual, 0, out,
                               (hipStream_t)stream);
+    if (type == Q6_K && prefill_q6k_fits(cols))
+        return prefill_q6k_launch(w, rows, cols, xq, xd, tokens, residual, out, (hipStream_t)stream);
     MmqArgs a = {};
     a.w[0] = a.w[1] = (const uint8_t*)w;
     a.out = out;

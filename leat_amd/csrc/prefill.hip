@@ -24,21 +24,18 @@
 // and the rows as N (operand B: lane l holds row l % 32, the same values); the int32 result in
 // lane l is row l % 32 for tokens 8(v / 4) + 4h + v % 4 of registers v. The f32 scale matrices
 // xd (x) (d * sc) of both token tiles come from one v_mfma_f32_32x32x1_2b_f32 (two outer
-// products), in the layout of D, so acc[v] += D[v] * S[v] is two VALU ops an element. The mins take one more f32 product per pair of groups: K = 2 is the pair (lane half h
-// supplies group 2j + h), added on the matrix cores straight into the sums at the end of a step.
-#include <type_traits>
-
+// products), in the layout of D, so acc[v] += D[v] * S[v] is two VALU ops an element. The mins
+// take one more f32 product per pair of groups: K = 2 is the pair (lane half h supplies group
+// 2j + h), added on the matrix cores straight into the sums at the end of a step.
 #include "blocks.h"
+#include "lds.h"
 #include "prefill.h"
 
 namespace leat {
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef float v32f __attribute__((ext_vector_type(32)));
+using namespace pf;
 
 constexpr int PF_WAVES = 4;
 constexpr int PF_TOKENS = 64;              // tokens per workgroup: two tiles of 32
@@ -49,8 +46,6 @@ constexpr int PF_X_BYTES = PF_TOKENS * 256;             // 16384: [16 chunks][64
 constexpr int PF_T_BYTES = 8 * PF_TOKENS * 4;           // one scale table: 2048, [8 groups][64 tokens]
 constexpr int PF_BUF = PF_W_BYTES + PF_X_BYTES + 2 * PF_T_BYTES;  // 38912
 constexpr int PF_LDS = 2 * PF_BUF;                      // 77824: two workgroups fit a CU
-
-enum PrefillMode : int { PF_PLAIN = 0, PF_RESIDUAL = 1, PF_GLU = 2 };
 
 struct PrefillArgs {
     const uint8_t* w[2];  // the GLU: gate, up
@@ -64,38 +59,6 @@ struct PrefillArgs {
     int row_tiles, token_tiles;  // workgroup tiles of PF_ROWS (the GLU: PF_ROWS / 2) rows and PF_TOKENS tokens
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(1))) void global_void;
-
-__device__ __forceinline__ void to_lds16(const void* src, uint32_t lds_at) {
-    __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)(uintptr_t)lds_at, 16, 0, 0);
-}
-__device__ __forceinline__ void to_lds4(const void* src, uint32_t lds_at) {
-    __builtin_amdgcn_global_load_lds((global_void*)src, (lds_void*)(uintptr_t)lds_at, 4, 0, 0);
-}
-
-__device__ __forceinline__ v16i mfma_i8(v4i a, u32x4 b) {
-    const v16i zero = {};
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, __builtin_bit_cast(v4i, b), zero, 0, 0, 0);
-}
-__device__ __forceinline__ v16f mfma_f32(float a, float b, v16f c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-// two outer products at once (v_mfma_f32_32x32x1_2b_f32): block k = lane half, its a[i] from
-// lane i + 32k, b[j] from lane j + 32k; block k's result in registers 16k.. in the 32x32 layout
-__device__ __forceinline__ v32f mfma_outer2(float a, float b) {
-    const v32f zero = {};
-    return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, zero, 0, 0, 0);
-}
-
-template <int K, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (K < N) {
-        f(std::integral_constant<int, K>{});
-        static_for<K + 1, N>(f);
-    }
-}
-
 // one group's operands (read from LDS) and products (matrix-core results) for the wave's two
 // token tiles
 struct GroupOps {
@@ -108,11 +71,6 @@ struct GroupRes {
     v16i D[2];
     v32f S;  // tile q's scales in registers 16q..16q+15
 };
-
-template <typename T>
-__device__ __forceinline__ T lds_read(uint32_t at) {
-    return *(const __attribute__((address_space(3))) T*)(uintptr_t)at;
-}
 
 // The lanes' fixed offsets of the direct loads: every load of a step is a uniform pointer (in
 // scalar registers) plus one of these.
@@ -178,7 +136,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
     v16f acc[2] = {};
 
     for (int step = 0; step < steps; step++) {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this step's direct loads are in LDS
+        wait_loads();                        // this step's direct loads are in LDS
         __syncthreads();                     // ... everyone's; and the other buffer is free
         const uint32_t buf = lds0 + (uint32_t)(step & 1) * PF_BUF;
         if (step + 1 < steps) stage<MODE>(a, so, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, step + 1, w);
