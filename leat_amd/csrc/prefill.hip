@@ -72,36 +72,62 @@ struct GroupRes {
     v32f S;  // tile q's scales in registers 16q..16q+15
 };
 
-// The lanes' fixed offsets of the direct loads: every load of a step is a uniform pointer (in
-// scalar registers) plus one of these.
+// The lanes' fixed parts of the direct loads. Every load reads consecutive bytes: one of weights
+// brings 64 consecutive 16-byte chunks of one matrix's 64 rows' step blocks (576 chunks, 9 loads),
+// which land row after row (row R's chunk p at byte 144 R + 16 p of the weights); one of
+// activations 4 tokens' 256 values; one of scales 8 tokens' 8 groups.
 struct StageOffsets {
-    uint32_t w[2];  // row (row0 + 64 half + lane)'s first byte in its matrix (the GLU: row0 + lane in both)
-    uint32_t x;     // token (tok0 + lane)'s first q8 byte
-    uint32_t t;     // token (tok0 + lane)'s first scale, in bytes
+    uint32_t w[5];    // weight loads i = w + 4u: chunk 64 (i % 9) + lane's byte past the step block of the load's first row
+    uint32_t xt, xc;  // activations: token lane / 16 of a load's 4; its source chunk (lane % 16) ^ (token % 16), in bytes
+    uint32_t tt;      // scales: token lane / 8 of a load's 8
+    uint32_t tg[2];   // ... and its source group (lane % 8) ^ s, for the loads s = w and w + 4
 };
 
+// row R (of 64) and chunk p of weight load i's lane `lane`
+__device__ __forceinline__ void chunk_of(int i, int lane, int& R, int& p) {
+    const int c = 64 * (i % 9) + lane;
+    R = c / 9;
+    p = c - 9 * R;
+}
+
 // Issues the direct loads of step `step` into the buffer at LDS address `buf`. An instruction
-// fills 64 consecutive 16-byte (or 4-byte) LDS slots, one per lane: weights chunk p of 64 rows
-// (slots [p][row]), activations chunk c of the 64 tokens (slots [c][token]), one group's scale of
-// the 64 tokens (slots [g][token]).
+// fills 64 consecutive 16-byte (or 4-byte) LDS slots, one per lane: the weights row after row
+// (matrix half i / 9: the GLU's up, else rows 64..127), the activations token after token (chunk
+// c of token t at chunk slot c ^ (t % 16)), the scales token after token (group s of token t at
+// slot s ^ (t / 8 % 8); xd of the 64 tokens, then xs).
 template <int MODE>
-__device__ __forceinline__ void stage(const PrefillArgs& a, const StageOffsets& o, uint32_t buf, int step, int w) {
-    for (int i = w; i < 18; i += PF_WAVES) {  // weights: chunk p = i % 9 of the rows of half i / 9
-        const int half = i >= 9, part = i - 9 * half;
+__device__ __forceinline__ void stage(const PrefillArgs& a, const StageOffsets& o, int row0, int tok0, bool full,
+                                      uint32_t buf, int step, int w) {
+    const uint32_t row_bytes = (uint32_t)(a.cols / 256) * PF_BLOCK;
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+        const int i = w + PF_WAVES * u;
+        if (i >= 18) break;
+        const int half = i >= 9;
         const uint8_t* m = MODE == PF_GLU && half ? a.w[1] : a.w[0];
-        to_lds16(m + (uint32_t)step * PF_BLOCK + 16 * part + o.w[half], buf + 2048 * part + 1024 * half);
+        const int first = row0 + (MODE == PF_GLU ? 0 : 64 * half);  // the load's first row
+        const uint8_t* src = m + (size_t)first * row_bytes + (uint32_t)step * PF_BLOCK + o.w[u];
+        if (!full) {  // a partial last tile: rows past the end read the last row
+            int R, p;
+            chunk_of(i, threadIdx.x & 63, R, p);
+            src = m + (size_t)min(first + R, a.rows - 1) * row_bytes + (uint32_t)step * PF_BLOCK + 16u * (uint32_t)p;
+        }
+        to_lds16(src, buf + 1024 * i);
     }
     const uint32_t xbase = buf + PF_W_BYTES, tbase = xbase + PF_X_BYTES;
 #pragma unroll
-    for (int u = 0; u < 16 / PF_WAVES; u++) {  // activations: chunk c of every token
-        const int c = w + PF_WAVES * u;
-        to_lds16((const uint8_t*)a.xq + 256 * step + 16 * c + o.x, xbase + 1024 * c);
+    for (int u = 0; u < 16 / PF_WAVES; u++) {  // activations: tokens 4i .. 4i + 3
+        const int i = w + PF_WAVES * u;
+        const size_t tok = (size_t)min(tok0 + 4 * i + (int)o.xt, a.tokens - 1);
+        to_lds16((const uint8_t*)a.xq + tok * a.cols + 256u * step + o.xc, xbase + 1024 * i);
     }
+    const int groups = a.cols / GROUP;
 #pragma unroll
-    for (int u = 0; u < 16 / PF_WAVES; u++) {  // scales: group g of xd (i < 8), then of xs
-        const int i = w + PF_WAVES * u, g = i & 7;
+    for (int u = 0; u < 16 / PF_WAVES; u++) {  // scales: xd (i < 8), then xs, of tokens 8s .. 8s + 7
+        const int i = w + PF_WAVES * u, s = i & 7;
         const float* tab = i < 8 ? a.xd : a.xs;
-        to_lds4((const uint8_t*)(tab + 8 * step + g) + o.t, tbase + 256 * i);
+        const size_t tok = (size_t)min(tok0 + 8 * s + (int)o.tt, a.tokens - 1);
+        to_lds4(tab + tok * groups + 8 * step + o.tg[u & 1], tbase + 256 * i);
     }
 }
 
@@ -124,14 +150,33 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
 
     StageOffsets so;
     {
-        const int half_rows = MODE == PF_GLU ? 0 : 64;
-        so.w[0] = (uint32_t)min(row0 + lane, a.rows - 1) * row_bytes;
-        so.w[1] = (uint32_t)min(row0 + half_rows + lane, a.rows - 1) * row_bytes;
-        const int tok = min(tok0 + lane, a.tokens - 1);
-        so.x = (uint32_t)tok * (uint32_t)a.cols;
-        so.t = (uint32_t)tok * (uint32_t)(a.cols / GROUP) * 4u;
+#pragma unroll
+        for (int u = 0; u < 5; u++) {
+            int R, p;
+            chunk_of(w + PF_WAVES * u, lane, R, p);
+            so.w[u] = (uint32_t)R * row_bytes + 16u * (uint32_t)p;
+        }
+        so.xt = (uint32_t)lane >> 4;
+        so.xc = 16u * (((uint32_t)lane & 15u) ^ ((4u * (uint32_t)w + ((uint32_t)lane >> 4)) & 15u));
+        so.tt = (uint32_t)lane >> 3;
+        so.tg[0] = ((uint32_t)lane & 7u) ^ (uint32_t)w;
+        so.tg[1] = ((uint32_t)lane & 7u) ^ (uint32_t)(w + PF_WAVES);
     }
-    stage<MODE>(a, so, lds0, 0, w);
+    const bool full = row0 + (MODE == PF_GLU ? 64 : 128) <= a.rows;
+    stage<MODE>(a, so, row0, tok0, full, lds0, 0, w);
+
+    // the lane's LDS offsets within a buffer: its row's weights (of the 128: gate or the first 64
+    // rows in waves 0, 1), token r's activations of tile q (chunk c = 2g + h at (xo ^ 32g) +
+    // 8192 q), xd of token r of tile h (group g at td ^ 4g) and xs of token r of tile q (group
+    // 2j + h at ts[q] ^ 8j)
+    const uint32_t wo = PF_BLOCK * (32 * w + r);
+    const uint32_t xo = PF_W_BYTES + 256u * r + ((16u * h) ^ (16u * (r & 15)));
+    constexpr uint32_t TB = PF_W_BYTES + PF_X_BYTES;
+    const uint32_t td = TB + 32u * (32 * h + r) + 4u * ((uint32_t)((32 * h + r) >> 3) & 7u);
+    uint32_t ts[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+        ts[q] = TB + PF_T_BYTES + 32u * (32 * q + r) + 4u * ((uint32_t)h ^ ((uint32_t)((32 * q + r) >> 3) & 7u));
 
     v16f acc[2] = {};
 
@@ -139,12 +184,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         wait_loads();                        // this step's direct loads are in LDS
         __syncthreads();                     // ... everyone's; and the other buffer is free
         const uint32_t buf = lds0 + (uint32_t)(step & 1) * PF_BUF;
-        if (step + 1 < steps) stage<MODE>(a, so, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, step + 1, w);
+        if (step + 1 < steps) stage<MODE>(a, so, row0, tok0, full, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, step + 1, w);
 
-        // lane (r, h)'s LDS bases: row 32w + r's chunks; token r's chunks of lane half h; token r's scales
-        const uint32_t wl = buf + 16 * (32 * w + r);
-        const uint32_t xl = buf + PF_W_BYTES + 1024 * h + 16 * r;
-        const uint32_t tl = buf + PF_W_BYTES + PF_X_BYTES + 4 * r;
+        const uint32_t wl = buf + wo;
         const u32x4 hdr = lds_read<u32x4>(wl);
         const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
 
@@ -159,7 +201,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
             const uint32_t mv = g < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
             const float mn = -dmin * (float)mv;
 #pragma unroll
-            for (int q = 0; q < 2; q++) acc[q] = mfma_f32(lds_read<float>(tl + PF_T_BYTES + 256 * g + 128 * q), mn, acc[q]);
+            for (int q = 0; q < 2; q++) acc[q] = mfma_f32(lds_read<float>(buf + (ts[q] ^ (8u * j))), mn, acc[q]);
         }
 
         // The step's 8 groups as a three-stage pipeline: the operands of group g + 2 are read from
@@ -170,7 +212,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         u32x4 qs = {};
         auto read = [&](auto gc) __attribute__((always_inline)) {
             constexpr int g = decltype(gc)::value;
-            if constexpr (g % 2 == 0) qs = lds_read<u32x4>(wl + 2048 * h + 2048 * (1 + g));  // chunk 1 + 2j + h
+            if constexpr (g % 2 == 0) qs = lds_read<u32x4>(wl + 16 * h + 16 * (1 + g));  // chunk 1 + 2j + h
             op[g].b = g % 2 ? ((qs >> 4) & 0x0F0F0F0Fu) : (qs & 0x0F0F0F0Fu);
             // get_scale_min_k4 (leat/quant.py:182-187): the group's 6-bit scale
             constexpr uint32_t sh = 8u * (g & 3);
@@ -179,9 +221,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
             op[g].wsc = d * (float)scv;
 #pragma unroll
             for (int q = 0; q < 2; q++) {
-                op[g].x[q] = lds_read<v4i>(xl + 512 * q + 2048 * g);  // chunk 2g + h of token t
+                op[g].x[q] = lds_read<v4i>(buf + (xo ^ (32u * g)) + 8192 * q);  // chunk 2g + h of token 32q + r
             }
-            op[g].xd = lds_read<float>(tl + 128 * h + 256 * g);
+            op[g].xd = lds_read<float>(buf + (td ^ (4u * g)));
         };
         auto issue = [&](auto gc) __attribute__((always_inline)) {
             constexpr int g = decltype(gc)::value;
