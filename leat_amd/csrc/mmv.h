@@ -20,6 +20,8 @@ struct MmvArgs {
     const float* xs;
     const float* residual;  // MMV_RESIDUAL: tokens * rows[0]
     int kind;               // MMV_GLU: w[0] gate, w[1] up, out[0]
+    int parts;              // set by mmv_launch: workgroups a tile's blocks are split over (1, or 2:
+                            // the two sums are added atomically into zeroed outputs)
 };
 
 enum MmvMode : int { MMV_PLAIN = 0, MMV_RESIDUAL = 1, MMV_GLU = 2 };

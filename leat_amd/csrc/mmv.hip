@@ -26,6 +26,7 @@
 #include <algorithm>
 
 #include "blocks.h"
+#include "lds.h"
 #include "mmv.h"
 
 namespace leat {
@@ -82,15 +83,15 @@ __device__ __forceinline__ void stage_load(Stage<TYPE>& st, const uint8_t* w, in
     const int64_t s0 = ((int64_t)stage * G::BPS * G::BYTES) & ~(int64_t)15;
 #pragma unroll
     for (int i = 0; i < Stage<TYPE>::N; i++) {
-        const int c = lane + 64 * i;
-        if (c < Stage<TYPE>::CHUNKS) {
-            const int r = c / G::CPR, part = c % G::CPR;
-            const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
-            // chunks past the row's end (the last stage's spare ones) repeat its last chunk
-            const uint32_t off = (uint32_t)min(s0 + 16 * part, row_bytes - 16);
-            // a 32-bit offset from the matrix's (uniform) start: matrices are under 4 GiB
-            st.v[i] = stream_load((const u32x4*)(w + (row * (uint32_t)row_bytes + off)));
-        }
+        // lanes past the stage's chunks load its last one (never stored): no branch around the
+        // load, so the wait for a stage's data counts exactly the loads issued after it
+        const int c = min(lane + 64 * i, Stage<TYPE>::CHUNKS - 1);
+        const int r = c / G::CPR, part = c % G::CPR;
+        const uint32_t row = (uint32_t)min(row0 + r, rows - 1);
+        // chunks past the row's end (the last stage's spare ones) repeat its last chunk
+        const uint32_t off = (uint32_t)min(s0 + 16 * part, row_bytes - 16);
+        // a 32-bit offset from the matrix's (uniform) start: matrices are under 4 GiB
+        st.v[i] = stream_load((const u32x4*)(w + (row * (uint32_t)row_bytes + off)));
     }
 }
 
@@ -102,7 +103,7 @@ __device__ __forceinline__ void stage_store(const Stage<TYPE>& st, uint32_t base
         const int c = lane + 64 * i;
         if (c < Stage<TYPE>::CHUNKS) {
             const int r = c / G::CPR, part = c % G::CPR;
-            *(u32x4*)((char*)mmv_lds + base + r * G::RS + 16 * part) = st.v[i];
+            *(u32x4*)__builtin_assume_aligned((char*)mmv_lds + base + r * G::RS + 16 * part, 16) = st.v[i];
         }
     }
 }
@@ -116,8 +117,9 @@ constexpr int token_slots() {
     return NV <= 2 ? 2 : NV == 4 ? 8 : 16;
 }
 
-template <int NV, bool XQ>
+template <int NV, bool XQ, int SETS_>
 struct Acts {
+    static constexpr int SETS = SETS_;
     static constexpr int TP = token_slots<NV>();
     const uint32_t* q;  // global words, when not XQ
     int cols;
@@ -131,11 +133,23 @@ struct Acts {
         lq = q + (int64_t)t * (cols / 4) + 4 * h;
         lx = (uint32_t)(xq_off + t * (cols / 4) + 4 * h);
     }
-    // the lane's 16 values of group g. A lane past the last token reads token 0's: its results
-    // (rows of tokens that are not there) are never stored, so no branch is needed here
-    __device__ v4i operand(int g) const {
+    // the lane's 16 values of group g, the stage's group s. A lane past the last token reads
+    // token 0's: its results (rows of tokens that are not there) are never stored, so no branch is
+    // needed here. From global memory, the stage's operands are loaded together beforehand (load).
+    static constexpr int GPS = 8;  // groups a stage
+    // (from global memory: SETS = 2 stages' sets, the next one's in flight while one is used,
+    // where the registers allow)
+    v4i ops[SETS ? SETS : 1][XQ || !SETS ? 1 : GPS];
+    __device__ __forceinline__ v4i operand(int g, int s, int set) const {
         if (XQ) return *(const v4i*)(mmv_lds + lx + g * 8);
-        return *(const v4i*)(lq + g * 8);
+        if (SETS == 0) return *(const v4i*)(lq + g * 8);  // one at a time (registers are short)
+        return ops[set % (SETS ? SETS : 1)][s];
+    }
+    template <int N>  // into `set`: the stage's N groups from g0
+    __device__ __forceinline__ void load(int set, int g0) {
+        if (!XQ && SETS > 0)
+#pragma unroll
+            for (int s = 0; s < N; s++) ops[set % SETS][s] = *(const v4i*)(lq + (g0 + s) * 8);
     }
     // the scales of group g for the lane's result registers v = 0..NV-1
     __device__ void scales(int off, int g, int h, float (&out)[NV]) const {
@@ -162,7 +176,7 @@ template <int TYPE> struct Compute;
 template <>
 struct Compute<Q4_K> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
+    __device__ __forceinline__ static void run(uint32_t base, int b, const A& a, int set, int r, int h, float (&acc)[NV]) {
         const uint32_t at = base + r * Geo<Q4_K>::RS;  // the block starts the chunk run
         const u32x4 hdr = lds16(at);
         const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
@@ -180,7 +194,7 @@ struct Compute<Q4_K> {
                 const uint32_t scv = s < 4 ? (x0 & 63u) : ((x2 & 15u) | ((x0 >> 2) & 0x30u));
                 const uint32_t mv = s < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
                 const float sc = d * (float)scv, mn = dmin * (float)mv;
-                const v16i D = mfma_i8(a.operand(g), e ? hi : lo);
+                const v16i D = mfma_i8(a.operand(g, s, set), e ? hi : lo);
                 float xd[NV], xs[NV];
                 a.scales(0, g, h, xd);
                 a.scales(a.s_off, g, h, xs);
@@ -196,15 +210,15 @@ struct Compute<Q4_K> {
 template <>
 struct Compute<Q6_K> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
+    __device__ __forceinline__ static void run(uint32_t base, int b, const A& a, int set, int r, int h, float (&acc)[NV]) {
         // odd blocks as a compile-time case: a run-time flag keeps both forms of every read live
         if (b & 1)
-            run_<NV, true>(base, b, a, r, h, acc);
+            run_<NV, true>(base, b, a, set, r, h, acc);
         else
-            run_<NV, false>(base, b, a, r, h, acc);
+            run_<NV, false>(base, b, a, set, r, h, acc);
     }
     template <int NV, bool ODD, class A>
-    __device__ static void run_(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
+    __device__ __forceinline__ static void run_(uint32_t base, int b, const A& a, int set, int r, int h, float (&acc)[NV]) {
         // the block starts (210 b) mod 16 bytes into the row's chunk run: 2 bytes off a 4-byte
         // boundary for odd b
         const uint32_t at = base + r * Geo<Q6_K>::RS + ((210u * (uint32_t)b) & 15u);
@@ -212,45 +226,104 @@ struct Compute<Q6_K> {
         const u32x4 scales = lds16_even(at + 192, odd);
         const uint32_t dword = lds4((at + 208) & ~3u);
         const float d = odd ? f16_hi(dword) : f16_lo(dword);
+        if constexpr (A::SETS != 2) {  // 1-2 tokens and the GLU (fewer registers): a group at a time
 #pragma unroll
-        for (int n = 0; n < 2; n++) {
-            const u32x4 qh = lds16_even(at + 128 + 32 * n + 16 * h, odd);
+            for (int n = 0; n < 2; n++) {
+                const u32x4 qh = lds16_even(at + 128 + 32 * n + 16 * h, odd);
 #pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const u32x4 ql = lds16_even(at + 64 * n + 32 * kk + 16 * h, odd);
+                for (int kk = 0; kk < 2; kk++) {
+                    const u32x4 ql = lds16_even(at + 64 * n + 32 * kk + 16 * h, odd);
 #pragma unroll
-                for (int k2 = 0; k2 < 2; k2++) {
-                    const int k = kk + 2 * k2;  // rows kk (low nibbles) and kk + 2 (high)
-                    const int g = 8 * b + 4 * n + k;
-                    u32x4 q;
+                    for (int k2 = 0; k2 < 2; k2++) {
+                        const int k = kk + 2 * k2;  // rows kk (low nibbles) and kk + 2 (high)
+                        const int g = 8 * b + 4 * n + k;
+                        u32x4 q;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t low = (ql[i] >> (4 * k2)) & 0x0F0F0F0Fu;
-                        const uint32_t high = (qh[i] >> (2 * k)) & 0x03030303u;
-                        q[i] = minus_bytes(low | (high << 4), 32);
+                        for (int i = 0; i < 4; i++) {
+                            const uint32_t low = (ql[i] >> (4 * k2)) & 0x0F0F0F0Fu;
+                            const uint32_t high = (qh[i] >> (2 * k)) & 0x03030303u;
+                            q[i] = minus_bytes(low | (high << 4), 32);
+                        }
+                        const v4i x = a.operand(g, 4 * n + k, set);
+                        const u32x4 zero = {};
+                        const v16i D0 = mfma_i8(x, h == 0 ? q : zero);  // values 0..15 of the row
+                        const v16i D1 = mfma_i8(x, h == 1 ? q : zero);  // values 16..31
+                        const int si = 8 * n + 2 * k;                   // scales si, si + 1
+                        const float s0 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3))) & 0xFF);
+                        const float s1 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3) + 8)) & 0xFF);
+                        float xd[NV];
+                        a.scales(0, g, h, xd);
+#pragma unroll
+                        for (int v = 0; v < NV; v++) acc[v] += xd[v] * (s0 * (float)D0[v] + s1 * (float)D1[v]);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    const v4i x = a.operand(g);
-                    const u32x4 zero = {};
-                    const v16i D0 = mfma_i8(x, h == 0 ? q : zero);  // values 0..15 of the row
-                    const v16i D1 = mfma_i8(x, h == 1 ? q : zero);  // values 16..31
-                    const int si = 8 * n + 2 * k;                   // scales si, si + 1
-                    const float s0 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3))) & 0xFF);
-                    const float s1 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3) + 8)) & 0xFF);
-                    float xd[NV];
-                    a.scales(0, g, h, xd);
-#pragma unroll
-                    for (int v = 0; v < NV; v++) acc[v] += xd[v] * (s0 * (float)D0[v] + s1 * (float)D1[v]);
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
+            return;
         }
+        // else the 8 groups (n = g / 4, k = g % 4: the rows k of half n) as a pipeline: the operands
+        // of group g + 2 are read and decoded while the products of g + 1 are issued and g is scaled
+        struct Op {
+            v4i x;
+            u32x4 q;
+            float s0, s1;
+            float xd[NV];
+        };
+        struct Res {
+            v16i D0, D1;
+        };
+        u32x4 qh[2], ql[2][2];
+        Op op[8];
+        Res rs[8];
+        auto prep = [&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value, n = g / 4, k = g % 4, kk = k & 1, k2 = k >> 1;
+            if constexpr (k == 0) {  // half n's bytes: qh, and ql of rows 0, 2 and 1, 3
+                qh[n] = lds16_even(at + 128 + 32 * n + 16 * h, odd);
+                ql[n][0] = lds16_even(at + 64 * n + 16 * h, odd);
+                ql[n][1] = lds16_even(at + 64 * n + 32 + 16 * h, odd);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t low = (ql[n][kk][i] >> (4 * k2)) & 0x0F0F0F0Fu;
+                const uint32_t high = (qh[n][i] >> (2 * k)) & 0x03030303u;
+                op[g].q[i] = minus_bytes(low | (high << 4), 32);
+            }
+            op[g].x = a.operand(8 * b + g, g, set);
+            constexpr int si = 8 * n + 2 * k;  // scales si, si + 1
+            op[g].s0 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3))) & 0xFF);
+            op[g].s1 = d * (float)(int8_t)((scales[si >> 2] >> (8 * (si & 3) + 8)) & 0xFF);
+            a.scales(0, 8 * b + g, h, op[g].xd);
+        };
+        auto issue = [&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value;
+            const u32x4 zero = {};
+            rs[g].D0 = mfma_i8(op[g].x, h == 0 ? op[g].q : zero);  // values 0..15 of the row
+            rs[g].D1 = mfma_i8(op[g].x, h == 1 ? op[g].q : zero);  // values 16..31
+        };
+        auto scale = [&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value;
+#pragma unroll
+            for (int v = 0; v < NV; v++)
+                acc[v] += op[g].xd[v] * (op[g].s0 * (float)rs[g].D0[v] + op[g].s1 * (float)rs[g].D1[v]);
+        };
+        prep(std::integral_constant<int, 0>{});
+        issue(std::integral_constant<int, 0>{});
+        prep(std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        pf::static_for<0, 8>([&](auto gc) __attribute__((always_inline)) {
+            constexpr int g = decltype(gc)::value;
+            if constexpr (g + 1 < 8) issue(std::integral_constant<int, g + 1>{});
+            if constexpr (g + 2 < 8) prep(std::integral_constant<int, g + 2>{});
+            scale(gc);
+            __builtin_amdgcn_sched_barrier(0);  // keeps two groups' results in registers, not eight
+        });
     }
 };
 
 template <>
 struct Compute<Q8_0> {
     template <int NV, class A>
-    __device__ static void run(uint32_t base, int b, const A& a, int r, int h, float (&acc)[NV]) {
+    __device__ __forceinline__ static void run(uint32_t base, int b, const A& a, int set, int r, int h, float (&acc)[NV]) {
         // a stage is blocks b and b + 1 (68 bytes from a 4-byte aligned start, b even)
         const uint32_t at = base + r * Geo<Q8_0>::RS + ((34u * (uint32_t)b) & 15u);
 #pragma unroll
@@ -259,7 +332,7 @@ struct Compute<Q8_0> {
             const uint32_t dword = lds4(blk & ~3u);
             const float d = e ? f16_hi(dword) : f16_lo(dword);
             const u32x4 qs = lds16_even(blk + 2 + 16 * h, e == 0);
-            const v16i D = mfma_i8(a.operand(b + e), qs);
+            const v16i D = mfma_i8(a.operand(b + e, e, set), qs);
             float xd[NV];
             a.scales(0, b + e, h, xd);
 #pragma unroll
@@ -268,6 +341,13 @@ struct Compute<Q8_0> {
         }
     }
 };
+
+#ifndef LEAT_MMV_DEPTH
+#define LEAT_MMV_DEPTH 1  // stages of loads a wave keeps in flight (1 or 2)
+#endif
+#ifndef LEAT_MMV_INTERLEAVE
+#define LEAT_MMV_INTERLEAVE 1  // the waves of a tile take every S-th stage (else runs of stages)
+#endif
 
 // waves per SIMD the register budget allows: 4 (128 registers) for one Q4_K or Q8_0 matrix and
 // up to two tokens' results, 3 (168) for Q6_K's wider stages, else 2 (256). A wave keeps a stage
@@ -301,7 +381,9 @@ void mmv_kernel(MmvArgs args) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 31, h = lane >> 5;
 
-    const int tile = blockIdx.x;
+    // the workgroup's tile, and its part of the tile's blocks (parts > 1: the first or second half)
+    const int part = (int)blockIdx.x / args.tile_start[args.count];
+    const int tile = (int)blockIdx.x - part * args.tile_start[args.count];
     int m = 0;
     if (MODE != MMV_GLU)
         while (m + 1 < args.count && tile >= args.tile_start[m + 1]) m++;
@@ -313,13 +395,26 @@ void mmv_kernel(MmvArgs args) {
 
     // the wave's stages, and the first one's loads before anything else
     const int stages = nb / G::BPS;
-    const int k0 = (int)((int64_t)stages * wave / S), k1 = (int)((int64_t)stages * (wave + 1) / S);
-    Stage<TYPE> st[NM];
-    if (k0 < k1)
+    const int p0 = stages * part / args.parts, pn = stages * (part + 1) / args.parts - p0;
+    // the wave's stages ka + ks j, j < nk: with LEAT_MMV_INTERLEAVE every S-th of the part's
+    // (the S waves read neighbouring blocks of the tile's rows at a time), else a run of them
+#if LEAT_MMV_INTERLEAVE
+    const int ka = p0 + wave, ks = S, nk = ka < p0 + pn ? (p0 + pn - ka + S - 1) / S : 0;
+#else
+    const int ka = p0 + pn * wave / S, ks = 1, nk = p0 + pn * (wave + 1) / S - ka;
+#endif
+    // stages j and (LEAT_MMV_DEPTH 2) j + 1 in flight
+    Stage<TYPE> st[LEAT_MMV_DEPTH][NM];
 #pragma unroll
-        for (int i = 0; i < NM; i++) stage_load<TYPE>(st[i], wm[i], row_bytes, row0, rows, k0, lane);
+    for (int p = 0; p < LEAT_MMV_DEPTH; p++)
+        if (p < nk)
+#pragma unroll
+            for (int i = 0; i < NM; i++) stage_load<TYPE>(st[p][i], wm[i], row_bytes, row0, rows, ka + ks * p, lane);
 
-    using A = Acts<NV, XQ>;
+    // operand sets: 2 (prefetched) for Q6_K's 3+ tokens outside the GLU; none (loaded when used)
+    // where the register budget is 128 (occupancy 4); else 1
+    using A = Acts<NV, XQ,
+                   TYPE == Q6_K && NV >= 4 && MODE != MMV_GLU ? 2 : mmv_occupancy(TYPE, MODE, NV) >= 4 ? 0 : 1>;
     constexpr int TP = A::TP;
     A acts;
     acts.q = (const uint32_t*)args.xq;
@@ -327,17 +422,45 @@ void mmv_kernel(MmvArgs args) {
     acts.s_off = G_ * TP;
     acts.xq_off = table_bytes<TYPE, NV>(cols) / 4;
     {
+        // the scales of the groups of the workgroup's blocks, U loads in flight per thread
         float* tab = (float*)mmv_lds;
-        for (int i = threadIdx.x; i < G_ * TP; i += blockDim.x) {
-            const int g = i / TP, tk = i % TP;
-            const bool in = tk < tokens;
-            tab[i] = in ? args.xd[tk * G_ + g] : 0.0f;
-            if (TYPE == Q4_K) tab[G_ * TP + i] = in ? args.xs[tk * G_ + g] : 0.0f;
+        constexpr int GPS = TYPE == Q8_0 ? 2 : 8;  // groups a stage
+        const int gb0 = p0 * GPS, n = pn * GPS * TP;
+        constexpr int U = NV >= 4 ? 8 : 2;
+        for (int base = threadIdx.x; base < n; base += U * blockDim.x) {
+            float vd[U], vs[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = base + u * (int)blockDim.x, g = gb0 + i / TP, tk = i % TP;
+                const bool in = i < n && tk < tokens;
+                vd[u] = in ? args.xd[tk * G_ + g] : 0.0f;
+                vs[u] = TYPE == Q4_K && in ? args.xs[tk * G_ + g] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = base + u * (int)blockDim.x;
+                if (i < n) {
+                    tab[gb0 * TP + i] = vd[u];
+                    if (TYPE == Q4_K) tab[(G_ + gb0) * TP + i] = vs[u];
+                }
+            }
         }
         if (XQ) {
             const int words = tokens * (cols / 4);
-            for (int i = threadIdx.x; i < words / 4; i += blockDim.x)
-                ((u32x4*)(mmv_lds + acts.xq_off))[i] = ((const u32x4*)args.xq)[i];
+            constexpr int V = NV >= 4 ? 4 : 1;
+            for (int base = threadIdx.x; base < words / 4; base += V * blockDim.x) {
+                u32x4 v[V];
+#pragma unroll
+                for (int u = 0; u < V; u++) {
+                    const int i = base + u * (int)blockDim.x;
+                    if (i < words / 4) v[u] = ((const u32x4*)args.xq)[i];
+                }
+#pragma unroll
+                for (int u = 0; u < V; u++) {
+                    const int i = base + u * (int)blockDim.x;
+                    if (i < words / 4) ((u32x4*)(mmv_lds + acts.xq_off))[i] = v[u];
+                }
+            }
         }
         __syncthreads();
     }
@@ -350,20 +473,36 @@ void mmv_kernel(MmvArgs args) {
 #pragma unroll
         for (int v = 0; v < NV; v++) acc[i][v] = 0.0f;
 
-    for (int k = k0; k < k1; k++) {
-        // the previous stage's LDS reads are done before its region is overwritten
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+    constexpr int GS = TYPE == Q8_0 ? 2 : 8;  // groups a stage
+    if (A::SETS == 2 && nk > 0) acts.template load<GS>(0, ka * GS);
+    constexpr int UNR = A::SETS == 2 ? 2 : LEAT_MMV_DEPTH;  // stages a loop turn: the sets alternate
+    for (int j0 = 0; j0 < nk; j0 += UNR) {
 #pragma unroll
-        for (int i = 0; i < NM; i++) stage_store<TYPE>(st[i], regions + (wave * NM + i) * 32 * G::RS, lane);
-        if (k + 1 < k1)
+        for (int p = 0; p < UNR; p++) {
+            // stage j: its registers go to the wave's LDS region and take the loads of stage
+            // j + DEPTH; its activation operands are set p, the next stage's go to set 1 - p
+            const int sp = p % LEAT_MMV_DEPTH, j = j0 + p, k = ka + ks * j;
+            if (j >= nk) break;
+            // (the last stage loads its own set again: no branch around loads, as above)
+            if (A::SETS == 1)
+                acts.template load<GS>(0, k * GS);  // this stage's, all in flight at once
+            else if (A::SETS == 2)
+                acts.template load<GS>(1 - p, (ka + ks * min(j + 1, nk - 1)) * GS);
+            // the previous stage's LDS reads are done before its region is overwritten
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int i = 0; i < NM; i++) stage_load<TYPE>(st[i], wm[i], row_bytes, row0, rows, k + 1, lane);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
+            for (int i = 0; i < NM; i++) stage_store<TYPE>(st[sp][i], regions + (wave * NM + i) * 32 * G::RS, lane);
 #pragma unroll
-        for (int i = 0; i < NM; i++)
-            Compute<TYPE>::template run<NV>(regions + (wave * NM + i) * 32 * G::RS, k * G::BPS, acts, r, h, acc[i]);
+            for (int i = 0; i < NM; i++)  // (past the last stage: the last again, never stored)
+                stage_load<TYPE>(st[sp][i], wm[i], row_bytes, row0, rows, ka + ks * min(j + LEAT_MMV_DEPTH, nk - 1), lane);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int i = 0; i < NM; i++)
+                Compute<TYPE>::template run<NV>(regions + (wave * NM + i) * 32 * G::RS, k * G::BPS, acts, p, r, h,
+                                                acc[i]);
+        }
     }
 
     // the S waves' sums of the tile, through LDS
@@ -395,11 +534,40 @@ void mmv_kernel(MmvArgs args) {
         const int64_t at = (int64_t)tok * rows + row_out;
         float y = acc[0][v];
         if (MODE == MMV_GLU) y = glu(args.kind, acc[0][v], acc[NM - 1][v]);
-        if (MODE == MMV_RESIDUAL) y += args.residual[at];
-        out[at] = y;
+        if (MODE == MMV_RESIDUAL && part == 0) y += args.residual[at];
+        if (MODE != MMV_GLU && args.parts > 1)
+            atomicAdd(out + at, y);  // into zero: 0 + a + b is a + b in either order
+        else
+            out[at] = y;
     }
 }
 
+// zeroes the launch's outputs before a tile's two parts add into them
+__global__ void mmv_zero(MmvArgs a) {
+    const int m = blockIdx.y;
+    const int64_t n = (int64_t)a.tokens * a.rows[m];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        a.out[m][i] = 0.0f;
+}
+
+#ifndef LEAT_MMV_S16
+#define LEAT_MMV_S16 0
+#endif
+#ifndef LEAT_MMV_KSPLIT
+#define LEAT_MMV_KSPLIT 1  // split the blocks of tiles over two workgroups when tiles are fewer than CUs
+#endif
+
+// the current device's CU count, read once per device
+static int cu_count() {
+    static int counts[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!counts[dev]) {
+        int n = 0;
+        counts[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return counts[dev];
+}
 #ifndef LEAT_MMV_WAVES
 #define LEAT_MMV_WAVES 4096  // waves a launch aims for: 16 per CU
 #endif
@@ -407,7 +575,11 @@ void mmv_kernel(MmvArgs args) {
 template <int TYPE, int MODE, int NV, int S>
 static int mmv_launch_s(MmvArgs& a, hipStream_t st) {
     constexpr int NM = MODE == MMV_GLU ? 2 : 1;
-    const int tiles = a.tile_start[a.count];
+    if (a.parts > 1) {
+        hipLaunchKernelGGL(mmv_zero, dim3(64, a.count), dim3(256), 0, st, a);
+        if (check_launch("mmv")) return -1;
+    }
+    const int tiles = a.tile_start[a.count] * a.parts;
     const size_t tables = table_bytes<TYPE, NV>(a.cols);
     const size_t words = (size_t)a.tokens * a.cols;
     const size_t stages = (size_t)S * NM * 32 * Geo<TYPE>::RS;
@@ -424,10 +596,18 @@ static int mmv_launch_s(MmvArgs& a, hipStream_t st) {
 
 template <int TYPE, int MODE, int NV>
 static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
-    const int tiles = a.tile_start[a.count];
     const int stages = a.cols / weights_per_block<TYPE>() / Geo<TYPE>::BPS;
+    // fewer tiles than CUs (a 4096-row down product: 128): two workgroups a tile, each half the
+    // blocks, so that every CU streams
+    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && a.tile_start[a.count] < cu_count() && stages >= 32 ? 2 : 1;
+    const int tiles = a.tile_start[a.count] * a.parts;
     // waves per tile: enough for the launch to fill the GPU, at most one per stage of a row
     const int want = (LEAT_MMV_WAVES + tiles - 1) / tiles;
+#if LEAT_MMV_S16
+    // few tiles (a 4096-row down product: 128): 16 waves a tile keep enough bytes in flight
+    if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1 && MODE != MMV_GLU && NV <= 4)
+        if (want >= 16 && stages >= 16) return mmv_launch_s<TYPE, MODE, NV, 16>(a, st);
+#endif
     if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1)
         if (want >= 8 && stages >= 8) return mmv_launch_s<TYPE, MODE, NV, 8>(a, st);
     if (want >= 4 && stages >= 4) return mmv_launch_s<TYPE, MODE, NV, 4>(a, st);
