@@ -202,8 +202,9 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
 #define LEAT_TILES 1  // 0: 3..8 tokens take the staged matrix-core kernels instead of the tile kernels
 #endif
 
-// one or two tokens: the row-streaming kernels; 3..8: the matrix-core tile kernels; more (16):
-// the staged matrix-core kernels where they fit the shape; else the v_dot4 kernels
+// one or two tokens: the row-streaming kernels; 3..8: the matrix-core tile kernels for the GLU,
+// the staged matrix-core kernels (mmv) for the rest; more (16): the staged ones where they fit
+// the shape; else the v_dot4 kernels
 template <int MODE>
 static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     const int nw = MODE == MODE_GLU ? 2 : a.count;
@@ -222,7 +223,10 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         r.hq = a.hq, r.hd = a.hd, r.hs = a.hs;
         return rows_launch(type, MODE, r, tokens, false, s);
     }
-    if (LEAT_TILES && tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
+    // 3..8 tokens: the GLU on the tile kernels; the plain and residual products (where they fit)
+    // on the staged ones, which measured faster for them
+    if (LEAT_TILES && tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw) &&
+        (MODE == MODE_GLU || !mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw))) {
         TileArgs t = {};
         for (int i = 0; i < MAX_MATS; i++) {
             t.w[i] = a.w[i];

@@ -553,6 +553,9 @@ __global__ void mmv_zero(MmvArgs a) {
 #ifndef LEAT_MMV_S16
 #define LEAT_MMV_S16 0
 #endif
+#ifndef LEAT_MMV_SPLIT_STAGES
+#define LEAT_MMV_SPLIT_STAGES 32  // the fewest stages (blocks) a row needs for the split
+#endif
 #ifndef LEAT_MMV_KSPLIT
 #define LEAT_MMV_KSPLIT 1  // split the blocks of tiles over two workgroups when tiles are fewer than CUs
 #endif
@@ -599,7 +602,9 @@ static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
     const int stages = a.cols / weights_per_block<TYPE>() / Geo<TYPE>::BPS;
     // fewer tiles than CUs (a 4096-row down product: 128): two workgroups a tile, each half the
     // blocks, so that every CU streams
-    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && a.tile_start[a.count] < cu_count() && stages >= 32 ? 2 : 1;
+    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && a.tile_start[a.count] < cu_count() && stages >= LEAT_MMV_SPLIT_STAGES
+                  ? 2
+                  : 1;
     const int tiles = a.tile_start[a.count] * a.parts;
     // waves per tile: enough for the launch to fill the GPU, at most one per stage of a row
     const int want = (LEAT_MMV_WAVES + tiles - 1) / tiles;
