@@ -248,21 +248,33 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     if (blockIdx.x == 0 && p == 0)
         for (int i = threadIdx.x; i < pairs; i += MOE_WAVES * 64) a.ids[i] = route_id[i], a.weights[i] = route_w[i];
 
-    // 2. the expert of pair p, and its members (the same in every thread: LDS reads)
+    // 2. the expert of pair p, and its members (the same in every wave): each lane tests one pair
+    // of a run of 64, and a wave-wide ballot counts and finds them
     const int e = route_id[p];  // route_token ids are always below `experts`
     int rank = 0;  // the pairs before p routed to e
-    for (int q = 0; q < p; q++) rank += route_id[q] == e;
-    if (rank % C != 0) return;  // the whole workgroup: an earlier pair's workgroup serves p
     int m[C], n = 0;  // p and the next C - 1 pairs routed to e (at most one a token)
 #pragma unroll
     for (int j = 0; j < C; j++) m[j] = p;
-    for (int q = p; q < pairs && n < C; q++)
-        if (route_id[q] == e) {
+    for (int base = 0; base < pairs && n < C; base += WAVE) {
+        uint64_t hit = __ballot(base + lane < pairs && route_id[base + lane] == e);
+        if (base + WAVE <= p) {
+            rank += __popcll(hit);
+            continue;
+        }
+        if (base <= p) {  // p's run: the pairs before p, then p and those after
+            const uint64_t before = (1ull << (p - base)) - 1;
+            rank += __popcll(hit & before);
+            hit &= ~before;
+        }
+        for (; hit && n < C; hit &= hit - 1) {
+            const int q = base + __ffsll((unsigned long long)hit) - 1;
 #pragma unroll
             for (int j = 0; j < C; j++)  // m[n] = q without indexing registers at run time
                 if (j == n) m[j] = q;
             n++;
         }
+    }
+    if (rank % C != 0) return;  // the whole workgroup: an earlier pair's workgroup serves p
 
     // 3. the rows' loads, then the members' activations
     const int row0 = row_base + w;  // the wave's rows: row0 + 8r
