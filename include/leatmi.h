@@ -5,7 +5,8 @@
  * All pointers are device pointers the caller owns. Weights are GGUF blocks exactly as stored:
  * a (rows, cols) matrix is rows * cols / elements blocks, row after row (leat/quant.py:234-251).
  * Return value: 0, or -1 with a message in leat_last_error() (bad type, shape or pointer, or a
- * failed launch). Reference paths below are in alkinun/leat.
+ * failed launch). Reference paths below are in alkinun/leat. An output may be its call's residual
+ * buffer (a residual stream updated in place); it must not overlap the call's other inputs.
  */
 #ifndef LEATMI_H
 #define LEATMI_H

@@ -602,7 +602,11 @@ static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
     const int stages = a.cols / weights_per_block<TYPE>() / Geo<TYPE>::BPS;
     // fewer tiles than CUs (a 4096-row down product: 128): two workgroups a tile, each half the
     // blocks, so that every CU streams
-    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && a.tile_start[a.count] < cu_count() && stages >= LEAT_MMV_SPLIT_STAGES
+    // (not when the output is the residual itself: zeroing it first would lose the residual)
+    const size_t n = (size_t)a.tokens * a.rows[0];
+    const bool in_place = MODE == MMV_RESIDUAL && a.residual < a.out[0] + n && a.out[0] < a.residual + n;
+    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && !in_place && a.tile_start[a.count] < cu_count() &&
+                      stages >= LEAT_MMV_SPLIT_STAGES
                   ? 2
                   : 1;
     const int tiles = a.tile_start[a.count] * a.parts;
