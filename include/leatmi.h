@@ -130,6 +130,15 @@ int leat_glu_matmul(int type, const void *gate, const void *up, int rows, int co
                     const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
                     float *out, void *stream);
 
+/* The same and, for the down product of leat/kernels/matmul.py:1069-1081 feed_forward(), the
+ * quantize_q8 of its outputs: hq (tokens * rows / 4 words), hd and hs (tokens * rows / 32),
+ * bit-identical to leat_quantize_q8 of out. rows a multiple of 32. For Q4_K the GLU kernel
+ * writes them itself, and out may be NULL (no f32 outputs); for other types out is required and
+ * a quantize launch follows. */
+int leat_glu_matmul_q8(int type, const void *gate, const void *up, int rows, int cols,
+                       const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
+                       float *out, int32_t *hq, float *hd, float *hs, void *stream);
+
 /* Replaces leat/kernels/experts.py:163-172 route() (_route_kernel, :132-160): for each of `tokens`
  * rows of scores (tokens, experts) f32, the `used` best experts by repeated argmax (ties to the
  * lower id; -inf and NaN count as the least finite score) as ids (tokens * used) int32, and the

@@ -36,6 +36,7 @@ SIGNATURES: dict[str, list] = {
     "leat_matvecs_f32": [_i, _p, _p, _p, _i, _p, _i, _p, _f, _p, _p],
     "leat_matvec_f32": [_i, _p, _i, _i, _p, _i, _p, _f, _p, _p, _p],
     "leat_glu_matvec_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
+    "leat_glu_matmul_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
     "leat_glu_matvec_f32": [_i, _p, _p, _i, _i, _p, _i, _p, _f, _i, _p, _p, _p, _p, _p],
 }
 

@@ -20,6 +20,7 @@
 
 #include "blocks.h"
 #include "prefill.h"
+#include "leatmi.h"
 
 namespace leat {
 
@@ -388,4 +389,22 @@ extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int r
     a.xq = xq, a.xd = xd, a.xs = xs;
     a.kind = kind;
     return mmq_dispatch<MMQ_GLU>(type, a, (hipStream_t)stream);
+}
+
+extern "C" int leat_glu_matmul_q8(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
+                                  const float* xd, const float* xs, int tokens, int kind, float* out, int32_t* hq,
+                                  float* hd, float* hs, void* stream) {
+    LEAT_REQUIRE(hq && hd && hs && rows % GROUP == 0 && (uintptr_t)hq % 16 == 0,
+                 "glu_matmul_q8: the q8 output needs d, s, rows in 32s and 16-byte aligned words");
+    if (type != Q4_K) {  // the GLU, then the quantizer on its f32 outputs
+        LEAT_REQUIRE(out, "glu_matmul_q8: type %d needs the f32 output", type);
+        if (leat_glu_matmul(type, gate, up, rows, cols, xq, xd, xs, tokens, kind, out, stream)) return -1;
+        return leat_quantize_q8(out, tokens, rows, nullptr, 0.0f, hq, hd, hs, stream);
+    }
+    if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, hd) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, hd))
+        return -1;
+    LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul_q8: unknown GLU kind %d", kind);
+    const void* ws[2] = {gate, up};
+    return prefill_launch(MMQ_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream,
+                          (uint32_t*)hq, hd, hs);
 }

@@ -30,6 +30,7 @@
 #include "blocks.h"
 #include "lds.h"
 #include "prefill.h"
+#include "q8.h"
 
 namespace leat {
 
@@ -56,6 +57,9 @@ struct PrefillArgs {
     const float* xs;
     const float* residual;
     int kind;
+    uint32_t* hq;  // the GLU: the q8 of its outputs (quantize_q8 of each token's row), or null
+    float* hd;
+    float* hs;
     int row_tiles, token_tiles;  // workgroup tiles of PF_ROWS (the GLU: PF_ROWS / 2) rows and PF_TOKENS tokens
 };
 
@@ -274,7 +278,53 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
             for (int v = 0; v < 16; v++) acc[q][v] = glu(a.kind, acc[q][v], xchg[((w * 2 + q) * 16 + v) * 64 + lane]);
     }
     const int row = row0 + wave_row;
-    if (row >= a.rows) return;
+    // the GLU's outputs quantized as quantize_q8 would (q8.h's arithmetic): the two gate waves
+    // put their outputs in LDS token by token (64 rows a token, padded to 68 floats), then each of
+    // their 128 threads quantizes one group of 32 rows of one token in its own registers
+    if (MODE == PF_GLU && a.hq) {
+        float* yt = (float*)pf_lds + 2 * 2 * 16 * 64;  // past the exchange area
+        constexpr int YS = 68;
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) yt[(32 * q + 8 * (v >> 2) + 4 * h + (v & 3)) * YS + wave_row] = acc[q][v];
+        __syncthreads();  // the two gate waves (waves 2 and 3 have ended, and a barrier waits for none)
+        const int tid = threadIdx.x, tl = tid >> 1, grp = tid & 1;  // token tl, rows 32 grp ..
+        const int t = tok0 + tl, first = row0 + 32 * grp;
+        if (t < a.tokens && first < a.rows) {
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 c = *(const float4*)(yt + tl * YS + 32 * grp + 4 * i);
+                v[4 * i] = c.x, v[4 * i + 1] = c.y, v[4 * i + 2] = c.z, v[4 * i + 3] = c.w;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+            const float scale = amax / 127.0f;
+            const float rs = __builtin_amdgcn_rcpf(scale);
+            int total = 0;
+            uint32_t word[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                uint32_t wv = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int qv = scale > 0.0f ? round_quotient(v[4 * i + k], scale, rs) : 0;
+                    total += qv;
+                    wv |= (uint32_t)(qv & 0xFF) << (8 * k);
+                }
+                word[i] = wv;
+            }
+            const size_t at = (size_t)t * a.rows + first;
+            u32x4* dst = (u32x4*)(a.hq + at / 4);
+            dst[0] = u32x4{word[0], word[1], word[2], word[3]};
+            dst[1] = u32x4{word[4], word[5], word[6], word[7]};
+            a.hd[at / GROUP] = scale;
+            a.hs[at / GROUP] = scale * (float)total;
+        }
+    }
+    if (row >= a.rows || !a.out) return;
 #pragma unroll
     for (int q = 0; q < 2; q++)
 #pragma unroll
@@ -309,8 +359,10 @@ int prefill_go(PrefillArgs& a, hipStream_t st) {
 }  // namespace
 
 int prefill_launch(int mode, const void* const* ws, int rows, int cols, const int32_t* xq, const float* xd,
-                   const float* xs, int tokens, const float* residual, int kind, float* out, hipStream_t st) {
+                   const float* xs, int tokens, const float* residual, int kind, float* out, hipStream_t st,
+                   uint32_t* hq, float* hd, float* hs) {
     PrefillArgs a = {};
+    a.hq = hq, a.hd = hd, a.hs = hs;
     a.w[0] = (const uint8_t*)ws[0];
     a.w[1] = (const uint8_t*)ws[mode == PF_GLU ? 1 : 0];
     a.out = out;
