@@ -9,7 +9,8 @@
 // supplies to v_mfma_i32_32x32x32_i8.
 //
 // Math, per group and 32x32 tile (tokens as M, rows as N): Df = the group's int8 product, Dh the
-// product over half 1 only (the weight operand masked in lane half 0). The group's int32 sum
+// product over half 1 only (the activation operand of lane half 0 read from a zeroed stretch of
+// LDS). The group's int32 sum
 // sc0 * (Df - Dh) + sc1 * Dh = sc0 * Df + (sc1 - sc0) * Dh is exact, and below 2^24 in magnitude,
 // so its f32 conversion is exact too. It is scaled by xd[token] * d[row] (one
 // v_mfma_f32_32x32x1_2b_f32 gives that matrix for a pair of groups) into the f32 sums, the
@@ -49,7 +50,8 @@ constexpr int P6_W_BYTES = P6_ROWS * P6_SLOT;                 // 17408
 constexpr int P6_X_BYTES = P6_TOKENS * 256;                   // 16384: [token][16 chunks, swizzled]
 constexpr int P6_T_BYTES = P6_TOKENS * 32;                    // 2048: [token][8 groups, swizzled]
 constexpr int P6_BUF = P6_W_BYTES + P6_X_BYTES + P6_T_BYTES;  // 35840, a multiple of 256
-constexpr int P6_LDS = 2 * P6_BUF;                            // 71680: two workgroups fit a CU
+constexpr int P6_ZERO = 2 * P6_BUF;                           // 256 zero bytes after the buffers
+constexpr int P6_LDS = P6_ZERO + 256;                         // 71936: two workgroups fit a CU
 static_assert(P6_W_BYTES % 256 == 0 && P6_BUF % 256 == 0, "swizzled slots need 256-byte aligned bases");
 
 struct P6Args {
@@ -99,6 +101,10 @@ __device__ __forceinline__ void p6_stage(const P6Args& a, const P6Lanes& o, int 
     }
 }
 
+// byte h of Q6_UPPER is (h - 2) << 4 as a signed byte, h = 0..3 the two high bits of a 6-bit q:
+// q - 32 is the low nibble of q with that upper nibble (a v_perm_b32 table lookup per byte)
+constexpr uint32_t Q6_UPPER = 0x1000F0E0u;
+
 // 16 bytes from `lead` (0 or 2) bytes into the 20 at c (4 words) and e (the next word)
 __device__ __forceinline__ u32x4 shift_bytes(u32x4 c, uint32_t e, uint32_t lead) {
     u32x4 r;
@@ -112,7 +118,8 @@ __device__ __forceinline__ u32x4 shift_bytes(u32x4 c, uint32_t e, uint32_t lead)
 // one group's operands and products
 struct P6Ops {
     v4i x;
-    u32x4 b, bh;  // the weights; only lane half 1's (half 0 zeroed)
+    v4i xh;  // the activations of lane half 1 (half 0: zeros)
+    u32x4 b;  // the weights
     int sc0, sdiff;
     float xd;  // even groups: xd of the lane's token for group g + lane half
 };
@@ -151,7 +158,9 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
     const uint32_t wo = P6_SLOT * m;
     const uint32_t xo = P6_W_BYTES + 256u * t + ((16u * h) ^ (16u * (t & 15)));
     const uint32_t to = P6_W_BYTES + P6_X_BYTES + 32u * t + 4u * ((uint32_t)h ^ ((uint32_t)(t >> 3) & 7u));
-    const uint32_t hmask = h ? ~0u : 0u;
+    // lane half 0 reads its operand of the half-1 product from the zeros (at zo ^ 32g)
+    const uint32_t xoh = h ? xo : 0u;
+    if (threadIdx.x < 64) ((uint32_t*)(p6_lds + P6_ZERO))[threadIdx.x] = 0u;  // before the first barrier
 
     v16f acc = {};
     for (int step = 0; step < a.steps; step++) {
@@ -160,6 +169,7 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
         const uint32_t buf = lds0 + (uint32_t)(step & 1) * P6_BUF;
         if (step + 1 < a.steps) p6_stage(a, o, row0, tok0, lds0 + (uint32_t)((step + 1) & 1) * P6_BUF, step + 1, w);
 
+        const uint32_t hbuf = h ? buf : lds0 + P6_ZERO;
         const uint32_t lead = 2u * (uint32_t)(step & 1);  // the block's first byte in its window
         const uint32_t wl = buf + wo, wq = wl + 16u * h;
         // the row's 16 scales and d: window bytes lead + 192 .. lead + 209
@@ -184,22 +194,23 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t low = (ql[k & 1][i] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
+                // q - 32 = low | 16 (high - 2): the upper nibble (high - 2) << 4 by byte lookup
                 const uint32_t high = (qh[i] >> (2 * k)) & 0x03030303u;
-                op[g].b[i] = minus_bytes(low | (high << 4), 32);
-                op[g].bh[i] = op[g].b[i] & hmask;
+                const uint32_t upper = __builtin_amdgcn_perm(Q6_UPPER, Q6_UPPER, high);
+                op[g].b[i] = ((ql[k & 1][i] >> (4 * (k >> 1))) & 0x0F0F0F0Fu) | upper;
             }
             // scales 8n + 2k and 8n + 2k + 1: bytes 2k % 4 and the next of word 2n + k / 2
             const uint32_t sw = sc4[2 * n + k / 2];
             op[g].sc0 = __builtin_amdgcn_sbfe(sw, 8 * ((2 * k) % 4), 8);
             op[g].sdiff = __builtin_amdgcn_sbfe(sw, 8 * ((2 * k) % 4) + 8, 8) - op[g].sc0;
             op[g].x = lds_read<v4i>(buf + (xo ^ (32u * g)));
+            op[g].xh = lds_read<v4i>(hbuf + (xoh ^ (32u * g)));
             if constexpr (g % 2 == 0) op[g].xd = lds_read<float>(buf + (to ^ (4u * g)));
         };
         auto issue = [&](auto gc) __attribute__((always_inline)) {
             constexpr int g = decltype(gc)::value;
             rs[g].Df = mfma_i8(op[g].x, op[g].b);
-            rs[g].Dh = mfma_i8(op[g].x, op[g].bh);
+            rs[g].Dh = mfma_i8(op[g].xh, op[g].b);
             if constexpr (g % 2 == 0) S[g / 2] = mfma_outer2(op[g].xd, d);  // xd[token] * d[row], groups g, g + 1
         };
         auto scale = [&](auto gc) __attribute__((always_inline)) {
