@@ -152,31 +152,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
             for (int t = 0; t < B; t++)
                 if (lane == r) glu_out[t][row0 - tile_row + STEP * r] = keep[r][t];
         __syncthreads();
-        if (threadIdx.x < 32 * B) {
-            const int t = threadIdx.x >> 5, i = threadIdx.x & 31;
-            const float v = glu_out[t][i];
-            float amax = fabsf(v);
-#pragma unroll
-            for (int s = 1; s < 32; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 32));
-            const float scale = amax / 127.0f;
-            const int q = scale > 0.0f ? (int)roundf(v / scale) : 0;
-            int total = q;
-#pragma unroll
-            for (int s = 1; s < 32; s <<= 1) total += __shfl_xor(total, s, 32);
-            // four consecutive lanes' values make a word, value 4w + i in byte i
-            const uint32_t b0 = (uint32_t)(q & 0xFF);
-            const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
-            const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
-            const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
-            const int total_rows = a.rows[0];
-            if ((i & 3) == 0)
-                a.hq[((int64_t)t * total_rows + 32 * tile + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            if (i == 0) {
-                const int64_t g = ((int64_t)t * total_rows + 32 * tile) / GROUP;
-                a.hd[g] = scale;
-                a.hs[g] = scale * (float)total;
-            }
-        }
+        store_group_q8<B>(glu_out, a.rows[0], tile, a.hq, a.hd, a.hs);
     }
 }
 
