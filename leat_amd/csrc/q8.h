@@ -18,14 +18,20 @@ namespace leat {
 // shared memory. The summation order is that of a 256-thread block whatever THREADS is, so every
 // kernel normalizes to the same bits: threads 0..255 sum float4 runs strided by 1024, each wave
 // reduces with DPP moves (wave_sum_dpp), then (w0 + w1) + (w2 + w3); further waves contribute nothing.
+// a float4's sum of squares, and its values normalized (times inv, times the norm weight): the
+// expressions every path uses, so all of them round alike
+__device__ __forceinline__ float sum_sq4(float4 v) { return v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w; }
+__device__ __forceinline__ float4 normed4(float4 v, float inv, float4 w) {
+    return make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+}
+
 template <int THREADS = 256>
 __device__ __forceinline__ float block_inv_rms(const float* __restrict__ xr, int n, float eps, float* partial) {
     const int tid = threadIdx.x;
     float ss = 0.0f;
     if (tid < 256)
         for (int at = tid * 4; at < n; at += 1024) {
-            const float4 v = *(const float4*)(xr + at);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            ss += sum_sq4(*(const float4*)(xr + at));
         }
     ss = wave_sum_dpp(ss);
     __syncthreads();  // `partial` may still be read from a previous row
@@ -91,13 +97,7 @@ __device__ __forceinline__ void quantize_row(const float* __restrict__ xr, int n
     const int tid = threadIdx.x;
     for (int at = tid * 4; at < n; at += 4 * THREADS) {  // n % 32 == 0: an octet is all in or all out
         float4 v = *(const float4*)(xr + at);
-        if (weight) {
-            const float4 wv = *(const float4*)(weight + at);
-            v.x = v.x * inv * wv.x;
-            v.y = v.y * inv * wv.y;
-            v.z = v.z * inv * wv.z;
-            v.w = v.w * inv * wv.w;
-        }
+        if (weight) v = normed4(v, inv, *(const float4*)(weight + at));
         float dv, sv;
         const uint32_t word = quantize4(v, &dv, &sv);
         q[at / 4] = word;
@@ -107,6 +107,64 @@ __device__ __forceinline__ void quantize_row(const float* __restrict__ xr, int n
         }
     }
 }
+
+// B rows of n <= 1024 * NX f32 values (and the norm weight), held in registers by threads
+// 0..255 of a block, the float4 at 4 tid + 1024 j: loaded before anything else the block asks
+// of memory, so that the norm and quantization wait for x alone. quantize() then writes what
+// block_inv_rms and quantize_row write, bit for bit: the same sums in the same order and the
+// same quantize4 of every float4.
+template <int B, int NX>
+struct RowsInRegs {
+    float4 v[B][NX], w[NX];
+
+    __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ weight, int n) {
+        const int tid = threadIdx.x;
+        if (tid >= 256) return;
+#pragma unroll
+        for (int j = 0; j < NX; j++) {
+            const int at = 4 * tid + 1024 * j;
+            if (at >= n) break;
+#pragma unroll
+            for (int t = 0; t < B; t++) v[t][j] = *(const float4*)(x + (int64_t)t * n + at);
+            if (weight) w[j] = *(const float4*)(weight + at);
+        }
+    }
+
+    // token t's 1/rms and q8 into q (words), d and s (the token's first word and group); every
+    // thread of the block (THREADS of them) calls it; `partial` as block_inv_rms's
+    template <int THREADS>
+    __device__ __forceinline__ void quantize(int t, const float* weight, float eps, int n, float* partial, uint32_t* q,
+                                             float* d, float* s) {
+        const int tid = threadIdx.x;
+        float inv = 1.0f;
+        if (weight) {
+            float ss = 0.0f;
+            if (tid < 256)
+#pragma unroll
+                for (int j = 0; j < NX; j++)
+                    if (4 * tid + 1024 * j < n) ss += sum_sq4(v[t][j]);
+            ss = wave_sum_dpp(ss);
+            __syncthreads();  // `partial` may still be read from a previous row
+            if ((tid & (WAVE - 1)) == 0) partial[tid / WAVE] = ss;
+            __syncthreads();
+            const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+            inv = 1.0f / sqrtf(total / (float)n + eps);
+        }
+        if (tid >= 256) return;
+#pragma unroll
+        for (int j = 0; j < NX; j++) {
+            const int at = 4 * tid + 1024 * j;  // n % 32 == 0: an octet is all in or all out
+            if (at >= n) break;
+            const float4 u = weight ? normed4(v[t][j], inv, w[j]) : v[t][j];
+            float dv, sv;
+            q[at / 4] = quantize4(u, &dv, &sv);
+            if ((tid & 7) == 0) {
+                d[at / GROUP] = dv;
+                s[at / GROUP] = sv;
+            }
+        }
+    }
+};
 
 // The q8 of one group of 32 consecutive outputs per token, as quantize_q8 would write it: value i
 // of token t is vals[t][i] (shared memory), and threads 32t + i of the block (t < B) quantize it
