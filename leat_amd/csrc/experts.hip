@@ -11,7 +11,9 @@
 //   once per launch, whatever the number of tokens sharing it.
 // experts_down: a wave per (token, row of the output). Its lanes take (slot, task) items across the
 //   token's `used` experts and sum weight * (row . hidden of the pair) (+ the row's bias), so the
-//   sum over slots stays inside one wave, in a fixed order, with no atomics.
+//   sum over slots stays inside one wave, in a fixed order, with no atomics. The slots' experts and
+//   weights are read once a wave (lane s: slot s); for one or two tokens each lane has the loads of
+//   4 items in flight together before it sums them.
 #include <cfloat>
 
 #include "blocks.h"
@@ -430,7 +432,9 @@ struct ExpertsDownArgs {
     float* out;             // tokens * rows
 };
 
-template <int TYPE>
+// U: items of a lane whose loads are in flight together (4 for 1-2 tokens, whose few waves leave
+// registers to spare; 1 for more, whose waves fill the GPU at a higher occupancy)
+template <int TYPE, int U>
 __global__ __launch_bounds__(256) void experts_down_kernel(ExpertsDownArgs a) {
     using T = Task<TYPE>;
     const int lane = threadIdx.x & (WAVE - 1);
@@ -438,24 +442,55 @@ __global__ __launch_bounds__(256) void experts_down_kernel(ExpertsDownArgs a) {
     const int t = blockIdx.y;
     if (row >= a.rows) return;
     const int tasks = a.cols / T::TASK_W, items = a.used * tasks;
+    // the token's experts and their weights, lane s holding slot s's (used <= 64), read once
+    int slot_e = 0;
+    float slot_w = 0.0f;
+    if (lane < a.used) {
+        const int p = t * a.used + lane;
+        slot_e = expert_of(a.ids, p, a.experts);
+        slot_w = a.weights[p];
+        if (a.scales) slot_w *= a.scales[slot_e];
+    }
+    // items lane, lane + 64, ... in that order, U at a time: every load first, then the sums
     float acc = 0.0f;
-    for (int it = lane; it < items; it += WAVE) {
-        const int slot = it / tasks, task = it - slot * tasks;
-        const int p = t * a.used + slot;
-        const int e = expert_of(a.ids, p, a.experts);
-        float weight = a.weights[p];
-        if (a.scales) weight *= a.scales[e];
-        const typename T::Dec d = T::decode(T::load(a.w, (int64_t)e * a.rows + row, a.cols, task), task);
-        const ActQ x = load_act<TYPE>(a.hq, a.hd, a.hs, a.cols, p, task);
-        float v = T::combine(d, x, T::dots(d, x));
-        if (a.bias && task == 0) v += a.bias[(int64_t)e * a.rows + row];
-        acc += weight * v;
+    for (int base = lane; base < items; base += WAVE * U) {
+        typename T::Raw raw[U];
+        ActQ x[U];
+        int task_of[U], e_of[U];
+        float w_of[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int it = min(base + WAVE * u, items - 1);  // past the end: loads in range, sums dropped
+            const int slot = it / tasks, task = it - slot * tasks;
+            e_of[u] = __shfl(slot_e, slot);
+            w_of[u] = __shfl(slot_w, slot);
+            task_of[u] = task;
+            raw[u] = T::load(a.w, (int64_t)e_of[u] * a.rows + row, a.cols, task);
+            x[u] = load_act<TYPE>(a.hq, a.hd, a.hs, a.cols, t * a.used + slot, task);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + WAVE * u < items) {
+                const typename T::Dec d = T::decode(raw[u], task_of[u]);
+                float v = T::combine(d, x[u], T::dots(d, x[u]));
+                if (a.bias && task_of[u] == 0) v += a.bias[(int64_t)e_of[u] * a.rows + row];
+                acc += w_of[u] * v;
+            }
+        }
     }
     acc = wave_sum(acc);
     if (lane == 0) {
         const int64_t at = (int64_t)t * a.rows + row;
         a.out[at] = a.residual ? acc + a.residual[at] : acc;
     }
+}
+
+template <int TYPE>
+static void experts_down_go(const dim3& grid, int tokens, hipStream_t st, const ExpertsDownArgs& a) {
+    if (tokens <= 2)
+        hipLaunchKernelGGL((experts_down_kernel<TYPE, 4>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((experts_down_kernel<TYPE, 1>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace leat
@@ -515,6 +550,7 @@ extern "C" int leat_experts_down(int type, const void* w, int experts, int rows,
                                  float* out, void* stream) {
     LEAT_REQUIRE(w && hq && hd && hs && ids && weights && out, "experts_down: null pointer");
     LEAT_REQUIRE(experts > 0 && rows > 0 && used > 0, "experts_down: empty experts");
+    LEAT_REQUIRE(used <= WAVE, "experts_down: %d experts a token (1..%d)", used, WAVE);
     LEAT_REQUIRE(tokens >= 0 && tokens <= 65535, "experts_down: %d tokens", tokens);
     if (check_cols(type, cols) || check_ptrs(type, w, hq)) return -1;
     if (tokens == 0) return 0;
@@ -526,9 +562,9 @@ extern "C" int leat_experts_down(int type, const void* w, int experts, int rows,
     const dim3 grid((rows + 3) / 4, tokens);
     hipStream_t st = (hipStream_t)stream;
     switch (type) {
-    case Q4_K: hipLaunchKernelGGL(experts_down_kernel<Q4_K>, grid, dim3(256), 0, st, a); break;
-    case Q6_K: hipLaunchKernelGGL(experts_down_kernel<Q6_K>, grid, dim3(256), 0, st, a); break;
-    case Q8_0: hipLaunchKernelGGL(experts_down_kernel<Q8_0>, grid, dim3(256), 0, st, a); break;
+    case Q4_K: experts_down_go<Q4_K>(grid, tokens, st, a); break;
+    case Q6_K: experts_down_go<Q6_K>(grid, tokens, st, a); break;
+    case Q8_0: experts_down_go<Q8_0>(grid, tokens, st, a); break;
     }
     return check_launch("experts_down");
 }
