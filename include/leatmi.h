@@ -176,7 +176,7 @@ int leat_experts_glu_f32(int type, const void *gate, const void *up, int experts
  * out[t * rows + r] = sum over slots s < used of weights[p] * scales[e] * (w[e] row r . h[p]
  * + bias[e * rows + r]) (+ residual[t * rows + r]), p = t * used + s, e = ids[p]; h the pairs'
  * hidden states as quantize_q8's (hq, hd, hs), tokens * used rows of cols. w: a stack of
- * `experts` (rows, cols) matrices. scales, bias and residual may be NULL. */
+ * `experts` (rows, cols) matrices. scales, bias and residual may be NULL. used 1..64. */
 int leat_experts_down(int type, const void *w, int experts, int rows, int cols, const int32_t *hq,
                       const float *hd, const float *hs, const int32_t *ids, const float *weights,
                       int tokens, int used, const float *scales, const float *bias,
