@@ -59,6 +59,9 @@ def test_rejects_bad_arguments(lib):
         _lib.call("leat_quantize_q8", one, 1, 33, None, 0.0, one, one, one, None)
     with pytest.raises(_lib.LeatError, match="null"):
         _lib.call("leat_matvec", 12, None, 4, 256, one, one, one, 1, None, one, None)
+    with pytest.raises(_lib.LeatError, match="65 experts a token"):  # a wave holds one slot a lane
+        _lib.call("leat_experts_down", 14, one, 128, 4, 512, one, one, one, one, one, 1, 65, None, None, None, one,
+                  None)  # fmt: skip
 
 
 def test_product_path_has_no_cpu_fallback():
