@@ -165,7 +165,8 @@ int leat_experts_glu(int type, const void *gate, const void *up, int experts, in
  * out[p * rows + r] as leat_experts_glu; out may be NULL. hq, hd, hs receive leat_quantize_q8 of
  * those pairs * rows values (rows a multiple of 32). Limits: experts <= 256, used <= 64; rows of
  * Q4_K (cols a multiple of 256), Q6_K (of 512) or Q8_0 (of 64) of at most 8192 weights; x and
- * norm_weight 16-byte aligned. An expert chosen by more than 2 tokens is read once per 2 of them. */
+ * norm_weight 16-byte aligned. An expert chosen by k tokens is read k times (one workgroup a pair:
+ * faster at 8 tokens than sharing its rows). */
 int leat_experts_glu_f32(int type, const void *gate, const void *up, int experts, int rows, int cols,
                          const float *x, int tokens, const float *norm_weight, float eps,
                          const float *scores, int used, const float *gate_bias, const float *up_bias,

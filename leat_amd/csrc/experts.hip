@@ -188,8 +188,9 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // 1. its 8 waves route every token (route_token, the routing kernel's arithmetic) into LDS, and
 //    workgroup (0, 0) publishes ids and weights for the down product;
 // 2. the pairs routed to one expert (at most one a token) are served C at a time, by the
-//    workgroups of the first, (C+1)-th, ... of them; the others exit. With C = 2 slots an expert
-//    is read once unless more than 2 tokens chose it;
+//    workgroups of the first, (C+1)-th, ... of them; the others exit. Launches take C = 1: an
+//    expert chosen by k tokens is read k times, but the workgroups' smaller register budget lets
+//    more of them run at once (8 tokens: 39 us a layer's launch against 45 with C = 2, 61 with 4);
 // 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
 //    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes the
 //    member tokens' x into LDS with the standalone quantizer's arithmetic (q8.h);
@@ -393,19 +394,10 @@ static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 4>), grid, dim3(MOE_WAVES * 64), lds, st, a);
 }
 
-// turns * token slots the members' activations may take in registers: Q6_K and Q8_0 blocks
-// decode into more registers than Q4_K's, so their rows of several turns take fewer tokens
-__host__ __device__ constexpr int moe_budget(int type, int turns) {
-    return type == Q4_K || (type == Q6_K && turns == 1) ? 8 : 4;
-}
-
-// member slots a pass: 2 (an expert rarely serves more tokens; the rest in further passes) where
-// they fit the registers, else 1
+// one member slot a pass (C = 1): faster than sharing an expert's rows between members
 template <int TYPE, int NT>
 static void moe_glu_c(MoeGluArgs& a, hipStream_t st) {
-    if constexpr (2 * NT <= moe_budget(TYPE, NT))
-        if (a.tokens > 1) return moe_glu_go<TYPE, NT, 2>(a, st);
-    return moe_glu_go<TYPE, NT, 1>(a, st);
+    moe_glu_go<TYPE, NT, 1>(a, st);
 }
 
 template <int TYPE>
