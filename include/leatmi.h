@@ -146,6 +146,13 @@ int leat_glu_matmul_q8(int type, const void *gate, const void *up, int rows, int
 int leat_route(const float *scores, int tokens, int experts, int used, int32_t *ids, float *weights,
                void *stream);
 
+/* Replaces leat/kernels/experts.py:110-124 scores() (_scores_kernel, :44-64): a mixture's router
+ * scores in f32, out[t * experts + e] = (sum_i x[t,i] * norm_weight[i] * router[e,i]) /
+ * sqrt(mean(x[t]^2) + eps), for x (tokens, dim) f32 and an F32 router (experts, dim). dim a
+ * multiple of 4; x, norm_weight and router 16-byte aligned. */
+int leat_scores(const float *x, int tokens, int dim, const float *norm_weight, float eps,
+                const float *router, int experts, float *out, void *stream);
+
 /* Replaces the expert kernel of leat/kernels/experts.py:341-359 (_experts_swiglu_kernel,
  * :209-238): out[p * rows + r] = glu(kind)(gate[e] row r . x[p / used] + gate_bias[e * rows + r],
  * up[e] row r . x[p / used] + up_bias[e * rows + r]) for pairs p < pairs, e = ids[p], x as

@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p],
     "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p],
     "leat_route": [_p, _i, _i, _i, _p, _p, _p],
+    "leat_scores": [_p, _i, _i, _p, _f, _p, _i, _p, _p],
     "leat_experts_glu": [_i, _p, _p, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p, _p],
     "leat_experts_down": [_i, _p, _i, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
     "leat_experts_glu_f32": [_i, _p, _p, _i, _i, _i, _p, _i, _p, _f, _p, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p],

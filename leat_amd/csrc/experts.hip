@@ -402,7 +402,8 @@ static void moe_glu_c(MoeGluArgs& a, hipStream_t st) {
 
 template <int TYPE>
 static void moe_glu_nt(MoeGluArgs& a, hipStream_t st) {
-    const int turns = a.cols / Task<TYPE>::TASK_W / WAVE;
+    // turns of a wave's 64 tasks, the last one possibly partial (has[] idles the lanes past it)
+    const int turns = (a.cols / Task<TYPE>::TASK_W + WAVE - 1) / WAVE;
     if (turns <= 1) return moe_glu_c<TYPE, 1>(a, st);
     if (turns <= 2) return moe_glu_c<TYPE, 2>(a, st);
     return moe_glu_c<TYPE, 4>(a, st);

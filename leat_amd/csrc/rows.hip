@@ -220,8 +220,7 @@ __global__ __launch_bounds__(KS * 64) void rows_split_kernel(RowsArgs a) {
 #pragma unroll
         for (int i = 0; i < KS; i++) y += part[i][t][r];
         const int64_t at = (int64_t)t * rows + row;
-        if (MODE == ROWS_RESIDUAL) y += a.residual[at];
-        if (row < rows) a.out[0][at] = y;
+        if (row < rows) a.out[0][at] = MODE == ROWS_RESIDUAL ? y + a.residual[at] : y;
     }
 }
 

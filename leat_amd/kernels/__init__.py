@@ -320,6 +320,34 @@ def route(scores: torch.Tensor, used: int) -> tuple[torch.Tensor, torch.Tensor]:
     return ids, weights
 
 
+def supports_scores(x: torch.Tensor, router: QTensor) -> bool:
+    """An F32 router whose rows are whole 16-byte loads (leat/kernels/experts.py:110-112), on a
+    gfx950 GPU."""
+    return router.type == GGMLType.F32 and router.shape[1] % 4 == 0 and _on_gfx950(x)
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    # t contiguous and 16-byte aligned (a view into a mapped file may be neither)
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def scores(x: torch.Tensor, norm: Norm, router: QTensor) -> torch.Tensor:
+    """The router's scores of the experts for tokens x (1, T, dim): rms_norm(x, *norm) @ router.T
+    in f32 (leat/kernels/experts.py:115-124), one kernel: the norm's sum of squares and the
+    router rows' dot products with x * weight, scaled by the inverse root mean square."""
+    _lib.require_device(x)
+    dim = x.shape[-1]
+    tokens, experts = _rows_of(x), router.shape[0]
+    src = _aligned(_f32(x).reshape(tokens, dim))
+    weight = _aligned(_f32(norm[0]))
+    table = _aligned(router.data.reshape(experts, dim).float())
+    out = torch.empty(tokens, experts, dtype=torch.float32, device=x.device)
+    _lib.call("leat_scores", src.data_ptr(), tokens, dim, weight.data_ptr(), float(norm[1]), table.data_ptr(),
+              experts, out.data_ptr(), _lib.stream(x.device))  # fmt: skip
+    return out.view(*x.shape[:-1], experts)
+
+
 def _decode_tasks_fit(ggml_type: GGMLType, length: int) -> bool:
     # a row length the decode tasks cover: whole 256-weight blocks, or pairs of Q8_0 blocks
     step = 64 if ggml_type == GGMLType.Q8_0 else 256
@@ -420,6 +448,6 @@ def mixture(
 
 __all__ = [
     "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
-    "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "supports_matmul", "supports_matvec",
-    "supports_mixture", "swiglu",
+    "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
+    "supports_mixture", "supports_scores", "swiglu",
 ]  # fmt: skip

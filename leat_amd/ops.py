@@ -1,5 +1,5 @@
 """leat's operators on quantized weights (leat/ops.py:18-182) for torch-ROCm tensors: linear,
-linears, feed_forward, mixture, glu and rms_norm, with the LEAT_KERNELS=ref switch.
+linears, feed_forward, router, mixture, glu and rms_norm, with the LEAT_KERNELS=ref switch.
 
 Every product goes one of three ways, chosen per call by `_plan`:
 - "decode": up to kernels.MATVEC_TOKENS tokens, on the matrix-vector kernels;
@@ -17,7 +17,7 @@ import os
 import torch
 
 from leat_amd import kernels
-from leat_amd.quant import QTensor
+from leat_amd.quant import NATIVE, QTensor
 
 # gpt-oss's SwiGLU: the sigmoid's slope and the clamp on gate and up (leat/kernels/common.py:21)
 OAI_ALPHA, OAI_LIMIT = 1.702, 7.0
@@ -68,6 +68,8 @@ def linears(
 def _reference_product(x: torch.Tensor, w: QTensor) -> torch.Tensor:
     # the reference path's x @ w.dequant(x.dtype).T with x in f32, not quantized
     tokens = x.numel() // x.shape[-1]
+    if w.type in NATIVE:  # F32, F16, BF16 weights are their own values
+        return x @ w.dequant(x.dtype).T
     if tokens <= kernels.MATVEC_TOKENS or tokens == kernels.FEW_TOKENS:
         return kernels.matvec_f32x(x, w).to(x.dtype)
     return x @ w.dequant(x.dtype).T
@@ -95,6 +97,16 @@ def feed_forward(
         g, u = linears(x, gate, up, norm=norm)
         hidden = glu(kind, g, u)
     return linear(hidden, down, residual=x if residual else None)
+
+
+def router(x: torch.Tensor, norm: Norm, w: QTensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """A mixture's router scores rms_norm(x, *norm) @ w.T, plus `bias` if given (leat/ops.py:80-87):
+    one f32 kernel for an F32 router, else the linear product of the normed x."""
+    if not reference_mode() and kernels.supports_scores(x, w):
+        scores = kernels.scores(x, norm, w)
+    else:
+        scores = linear(rms_norm(x, *norm), w)
+    return scores if bias is None else scores + bias
 
 
 def mixture(
