@@ -284,12 +284,12 @@ def measure_prefill(torch, lib, w, reps, device):
         xq, xd, xs = q8[HIDDEN]
         hq, hd, hs = q8[FFN]
         _call(lib, "leat_glu_matmul_q8", Q4_K, w["gate"].data_ptr(), w["up"].data_ptr(), FFN, HIDDEN, xq.data_ptr(),
-              xd.data_ptr(), xs.data_ptr(), T, 0, None, hq.data_ptr(), hd.data_ptr(), hs.data_ptr(), st())  # fmt: skip
+              xd.data_ptr(), xs.data_ptr(), T, 0, None, hq.data_ptr(), hd.data_ptr(), hs.data_ptr(), None, 0, st())  # fmt: skip
 
     def down():
         hq, hd, hs = q8[FFN]
         _call(lib, "leat_matmul", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, hq.data_ptr(), hd.data_ptr(),
-              hs.data_ptr(), T, x.data_ptr(), out.data_ptr(), st())  # fmt: skip
+              hs.data_ptr(), T, x.data_ptr(), out.data_ptr(), None, 0, st())  # fmt: skip
 
     def ffn():
         quantize(x, HIDDEN, True)

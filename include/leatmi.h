@@ -43,7 +43,8 @@ int leat_quantize_q8(const float *x, int rows, int n, const float *norm_weight, 
 /* Replaces the custom kernel of leat/kernels/matvec.py:362-380 matvecs() for one matrix
  * (_matvec_kernel, :306-321): out[t * rows + r] = W[r] . x[t] (+ residual[t * rows + r] if
  * residual is not NULL), x given as quantize_q8's (xq, xd, xs) for `tokens` rows of `cols`
- * values. tokens: 1..8 or 16. cols: a multiple of 256 for Q4_K/Q6_K, of 64 for Q8_0. */
+ * values. tokens: 1..8, or up to 16 where the matrix-core decode kernels take the shape (16-byte
+ * aligned rows and matrices). cols: a multiple of 256 for Q4_K/Q6_K, of 64 for Q8_0. */
 int leat_matvec(int type, const void *w, int rows, int cols, const int32_t *xq, const float *xd,
                 const float *xs, int tokens, const float *residual, float *out, void *stream);
 
@@ -115,29 +116,40 @@ int leat_dequantize(int type, const void *blocks, int64_t n_blocks, float *out, 
 int leat_group_dots(int type, const void *w, int rows, int cols, const int32_t *xq, int tokens,
                     int32_t *out, void *stream);
 
+/* The bytes of workspace leat_matmul (gated = 0) or leat_glu_matmul / leat_glu_matmul_q8
+ * (gated = 1) split a product of this shape into, on the current device; 0 when it runs unsplit.
+ * Replaces the parts buffer of leat/kernels/matmul.py:1005-1010 (_products with a schedule). */
+int64_t leat_matmul_workspace(int type, int rows, int cols, int tokens, int gated);
+
 /* Replaces the custom kernel of leat/kernels/matmul.py:1051-1066 matmuls() (_matmul_kernel,
- * :631-841, with its fixup :856-901) for many tokens: out[t * rows + r] = W[r] . x[t]
+ * :631-841, with its schedule and fixup :856-964) for many tokens: out[t * rows + r] = W[r] . x[t]
  * (+ residual), x as quantize_q8's (xq, xd, xs) for `tokens` rows of `cols`. int8 products per
- * group of 32 on matrix cores, scaled per group in f32. cols a multiple of 256 (512 for Q6_K);
- * weights 4-byte (Q4_K: 16-byte) and xq 16-byte aligned. */
+ * group of 32 on matrix cores, scaled per group in f32. Up to 16 tokens (leat's FEW_TOKENS) take
+ * 32-row by 16-token tiles; more take 64-token tiles, and when those are fewer than the GPU runs
+ * at once each tile's K steps are split over several workgroups, their sums left in `workspace`
+ * (leat_matmul_workspace bytes; with less, or NULL, the product runs unsplit) and added by a
+ * fixup launch in a fixed order. cols a multiple of 256 (512 for Q6_K); weights 4-byte (Q4_K:
+ * 16-byte) and xq 16-byte aligned. */
 int leat_matmul(int type, const void *w, int rows, int cols, const int32_t *xq, const float *xd,
-                const float *xs, int tokens, const float *residual, float *out, void *stream);
+                const float *xs, int tokens, const float *residual, float *out, void *workspace,
+                int64_t workspace_bytes, void *stream);
 
 /* Replaces the gated product of leat/kernels/matmul.py:1069-1081 feed_forward() (_products with
  * gated=True): out[t * rows + r] = glu(kind)(gate[r] . x[t], up[r] . x[t]), gate and up in one
- * kernel. Same shape rules as leat_matmul. */
+ * kernel. Same shape, tile and workspace rules as leat_matmul. */
 int leat_glu_matmul(int type, const void *gate, const void *up, int rows, int cols,
                     const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
-                    float *out, void *stream);
+                    float *out, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* The same and, for the down product of leat/kernels/matmul.py:1069-1081 feed_forward(), the
  * quantize_q8 of its outputs: hq (tokens * rows / 4 words), hd and hs (tokens * rows / 32),
- * bit-identical to leat_quantize_q8 of out. rows a multiple of 32. For Q4_K the GLU kernel
- * writes them itself, and out may be NULL (no f32 outputs); for other types out is required and
- * a quantize launch follows. */
+ * bit-identical to leat_quantize_q8 of out. rows a multiple of 32. For Q4_K past 16 tokens the
+ * GLU kernel writes them itself, and out may be NULL (no f32 outputs); otherwise out is required
+ * and a quantize launch follows. */
 int leat_glu_matmul_q8(int type, const void *gate, const void *up, int rows, int cols,
                        const int32_t *xq, const float *xd, const float *xs, int tokens, int kind,
-                       float *out, int32_t *hq, float *hd, float *hs, void *stream);
+                       float *out, int32_t *hq, float *hd, float *hs, void *workspace,
+                       int64_t workspace_bytes, void *stream);
 
 /* Replaces leat/kernels/experts.py:163-172 route() (_route_kernel, :132-160): for each of `tokens`
  * rows of scores (tokens, experts) f32, the `used` best experts by repeated argmax (ties to the

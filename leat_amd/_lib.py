@@ -27,8 +27,9 @@ SIGNATURES: dict[str, list] = {
     "leat_matvec_f32x": [_i, _p, _i, _i, _p, _i, _p, _p, _p],
     "leat_dequantize": [_i, _p, _i64, _p, _p],
     "leat_group_dots": [_i, _p, _i, _i, _p, _i, _p, _p],
-    "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p],
-    "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p],
+    "leat_matmul_workspace": [_i, _i, _i, _i, _i],
+    "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p, _i64, _p],
+    "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _i64, _p],
     "leat_route": [_p, _i, _i, _i, _p, _p, _p],
     "leat_scores": [_p, _i, _i, _p, _f, _p, _i, _p, _p],
     "leat_experts_glu": [_i, _p, _p, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p, _p],
@@ -37,7 +38,7 @@ SIGNATURES: dict[str, list] = {
     "leat_matvecs_f32": [_i, _p, _p, _p, _i, _p, _i, _p, _f, _p, _p],
     "leat_matvec_f32": [_i, _p, _i, _i, _p, _i, _p, _f, _p, _p, _p],
     "leat_glu_matvec_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
-    "leat_glu_matmul_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
+    "leat_glu_matmul_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _i64, _p],
     "leat_glu_matvec_f32": [_i, _p, _p, _i, _i, _p, _i, _p, _f, _i, _p, _p, _p, _p, _p],
 }
 
@@ -59,6 +60,7 @@ def lib() -> ctypes.CDLL:
     handle.leat_last_error.restype = ctypes.c_char_p
     handle.leat_target.restype = ctypes.c_char_p
     handle.leat_abi_version.restype = ctypes.c_int
+    handle.leat_matmul_workspace.restype = ctypes.c_int64
     return handle
 
 
@@ -66,6 +68,11 @@ def call(name: str, *args) -> None:
     status = getattr(lib(), name)(*args)
     if status != 0:
         raise LeatError(f"{name}: {lib().leat_last_error().decode()}")
+
+
+def workspace_bytes(ggml_type: int, rows: int, cols: int, tokens: int, gated: bool) -> int:
+    """The workspace a prefill product of this shape splits into on the current device (0: none)."""
+    return int(lib().leat_matmul_workspace(int(ggml_type), rows, cols, tokens, int(gated)))
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -28,7 +28,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* leat_last_error(void) { return leat::last_error; }
 
-extern "C" int leat_abi_version(void) { return 1; }
+extern "C" int leat_abi_version(void) { return 2; }
 
 // The compiled device architecture of this library's kernels, to check against the device.
 extern "C" const char* leat_target(void) { return "gfx950"; }

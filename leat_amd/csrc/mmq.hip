@@ -19,8 +19,9 @@
 #include <algorithm>
 
 #include "blocks.h"
-#include "prefill.h"
 #include "leatmi.h"
+#include "mmv.h"
+#include "prefill.h"
 
 namespace leat {
 
@@ -351,36 +352,95 @@ static int mmq_check(int type, const void* w, int rows, int cols, const int32_t*
     return 0;
 }
 
-}  // namespace leat
+// the split of a launch of `tiles` tiles (prefill.h): chunks double while the launch still fits the
+// GPU's workgroup slots (two a CU) and every chunk keeps at least 4 of the `steps` K steps
+Split split_schedule(int tiles, int steps, int64_t part_bytes) {
+    const int slots = 2 * cu_count();
+    int chunks = 1;
+    while (chunks < 8 && (int64_t)tiles * chunks * 2 <= slots && steps >= 4 * chunks * 2) chunks *= 2;
+    return Split{chunks, chunks > 1 ? (int64_t)tiles * chunks * part_bytes : 0};
+}
 
-using namespace leat;
+// leat's tile height choice (leat/kernels/matmul.py:904-906, _tile_tokens): up to FEW_TOKENS
+// tokens take the matrix-core decode kernels, whose tiles are 32 rows by 16 tokens
+constexpr int FEW_TOKENS = 16;
 
-extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd,
-                           const float* xs, int tokens, const float* residual, float* out, void* stream) {
+static bool few_fits(int type, int cols, int tokens, const void* const* ws, int count) {
+    return tokens <= FEW_TOKENS && mmv_fits(type, cols, tokens, ws, count);
+}
+
+static int few_launch(int type, int mode, const void* const* ws, int count, int rows, int cols, const int32_t* xq,
+                      const float* xd, const float* xs, int tokens, const float* residual, int kind, float* out,
+                      hipStream_t st) {
+    MmvArgs m = {};
+    for (int i = 0; i < count; i++) m.w[i] = (const uint8_t*)ws[i];
+    m.out[0] = out;
+    m.rows[0] = rows;
+    m.count = 1;
+    m.cols = cols;
+    m.tokens = tokens;
+    m.xq = xq, m.xd = xd, m.xs = xs;
+    m.residual = residual;
+    m.kind = kind;
+    return mmv_launch(type, mode, m, st);
+}
+
+// the workspace a product would split into (0: it does not split)
+static int64_t workspace_of(int type, int rows, int cols, int tokens, bool gated) {
+    if (tokens <= FEW_TOKENS) return 0;  // the decode kernels (few_launch) take no workspace
+    if (type == Q4_K) return prefill_split(gated ? PF_GLU : PF_PLAIN, rows, cols, tokens).bytes;
+    if (type == Q6_K && !gated && prefill_q6k_fits(cols)) return prefill_q6k_split(rows, cols, tokens).bytes;
+    return 0;
+}
+
+int matmul_go(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd, const float* xs,
+              int tokens, const float* residual, float* out, void* workspace, int64_t workspace_bytes, hipStream_t st) {
     if (mmq_check(type, w, rows, cols, xq, xd, xs, tokens, out)) return -1;
+    if (few_fits(type, cols, tokens, &w, 1))
+        return few_launch(type, residual ? MMV_RESIDUAL : MMV_PLAIN, &w, 1, rows, cols, xq, xd, xs, tokens, residual, 0,
+                          out, st);
     if (type == Q4_K)
-        return prefill_launch(MMQ_RESIDUAL * (residual != nullptr), &w, rows, cols, xq, xd, xs, tokens, residual, 0, out,
-                              (hipStream_t)stream);
+        return prefill_launch(residual ? PF_RESIDUAL : PF_PLAIN, &w, rows, cols, xq, xd, xs, tokens, residual, 0, out, st,
+                              nullptr, nullptr, nullptr, workspace, workspace_bytes);
     if (type == Q6_K && prefill_q6k_fits(cols))
-        return prefill_q6k_launch(w, rows, cols, xq, xd, tokens, residual, out, (hipStream_t)stream);
+        return prefill_q6k_launch(w, rows, cols, xq, xd, tokens, residual, out, st, workspace, workspace_bytes);
     MmqArgs a = {};
     a.w[0] = a.w[1] = (const uint8_t*)w;
     a.out = out;
     a.rows = rows, a.cols = cols, a.tokens = tokens;
     a.xq = xq, a.xd = xd, a.xs = xs;
     a.residual = residual;
-    return residual ? mmq_dispatch<MMQ_RESIDUAL>(type, a, (hipStream_t)stream)
-                    : mmq_dispatch<MMQ_PLAIN>(type, a, (hipStream_t)stream);
+    return residual ? mmq_dispatch<MMQ_RESIDUAL>(type, a, st) : mmq_dispatch<MMQ_PLAIN>(type, a, st);
+}
+
+}  // namespace leat
+
+using namespace leat;
+
+extern "C" int64_t leat_matmul_workspace(int type, int rows, int cols, int tokens, int gated) {
+    if (rows <= 0 || cols <= 0 || tokens <= 0 || cols % 256 != 0) return 0;
+    return workspace_of(type, rows, cols, tokens, gated != 0);
+}
+
+extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd,
+                           const float* xs, int tokens, const float* residual, float* out, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+    return matmul_go(type, w, rows, cols, xq, xd, xs, tokens, residual, out, workspace, workspace_bytes,
+                     (hipStream_t)stream);
 }
 
 extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
-                               const float* xd, const float* xs, int tokens, int kind, float* out, void* stream) {
+                               const float* xd, const float* xs, int tokens, int kind, float* out, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
     if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, out) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, out))
         return -1;
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul: unknown GLU kind %d", kind);
     const void* ws[2] = {gate, up};
+    if (few_fits(type, cols, tokens, ws, 2))
+        return few_launch(type, MMV_GLU, ws, 2, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream);
     if (type == Q4_K)
-        return prefill_launch(MMQ_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream);
+        return prefill_launch(PF_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream,
+                              nullptr, nullptr, nullptr, workspace, workspace_bytes);
     MmqArgs a = {};
     a.w[0] = (const uint8_t*)gate;
     a.w[1] = (const uint8_t*)up;
@@ -393,18 +453,21 @@ extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int r
 
 extern "C" int leat_glu_matmul_q8(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
                                   const float* xd, const float* xs, int tokens, int kind, float* out, int32_t* hq,
-                                  float* hd, float* hs, void* stream) {
+                                  float* hd, float* hs, void* workspace, int64_t workspace_bytes, void* stream) {
     LEAT_REQUIRE(hq && hd && hs && rows % GROUP == 0 && (uintptr_t)hq % 16 == 0,
                  "glu_matmul_q8: the q8 output needs d, s, rows in 32s and 16-byte aligned words");
-    if (type != Q4_K) {  // the GLU, then the quantizer on its f32 outputs
+    const void* ws[2] = {gate, up};
+    // few tokens (with the f32 output given), and types the Q4_K kernel does not take: the GLU,
+    // then the quantizer on its f32 outputs
+    if (type != Q4_K || (out && few_fits(type, cols, tokens, ws, 2))) {
         LEAT_REQUIRE(out, "glu_matmul_q8: type %d needs the f32 output", type);
-        if (leat_glu_matmul(type, gate, up, rows, cols, xq, xd, xs, tokens, kind, out, stream)) return -1;
+        if (leat_glu_matmul(type, gate, up, rows, cols, xq, xd, xs, tokens, kind, out, workspace, workspace_bytes, stream))
+            return -1;
         return leat_quantize_q8(out, tokens, rows, nullptr, 0.0f, hq, hd, hs, stream);
     }
     if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, hd) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, hd))
         return -1;
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul_q8: unknown GLU kind %d", kind);
-    const void* ws[2] = {gate, up};
-    return prefill_launch(MMQ_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream,
-                          (uint32_t*)hq, hd, hs);
+    return prefill_launch(PF_GLU, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream,
+                          (uint32_t*)hq, hd, hs, workspace, workspace_bytes);
 }

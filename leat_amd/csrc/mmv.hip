@@ -24,6 +24,7 @@
 //         bits 2k), minus 32. u += d*sc*xd*D per half.
 //   Q8_0  one block is one group: lane h takes bytes [2 + 16h, +16). u += d*xd*D.
 #include <algorithm>
+#include <atomic>
 
 #include "blocks.h"
 #include "lds.h"
@@ -560,16 +561,19 @@ __global__ void mmv_zero(MmvArgs a) {
 #define LEAT_MMV_KSPLIT 1  // split the blocks of tiles over two workgroups when tiles are fewer than CUs
 #endif
 
-// the current device's CU count, read once per device
-static int cu_count() {
-    static int counts[64] = {};
+// the current device's CU count, read once per device; callers on several threads may race to
+// fill an entry, and all store the same value
+int cu_count() {
+    static std::atomic<int> counts[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!counts[dev]) {
+    int known = counts[dev].load(std::memory_order_relaxed);
+    if (!known) {
         int n = 0;
-        counts[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        known = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        counts[dev].store(known, std::memory_order_relaxed);
     }
-    return counts[dev];
+    return known;
 }
 #ifndef LEAT_MMV_WAVES
 #define LEAT_MMV_WAVES 4096  // waves a launch aims for: 16 per CU

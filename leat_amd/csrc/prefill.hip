@@ -61,7 +61,13 @@ struct PrefillArgs {
     float* hd;
     float* hs;
     int row_tiles, token_tiles;  // workgroup tiles of PF_ROWS (the GLU: PF_ROWS / 2) rows and PF_TOKENS tokens
+    // split products (chunks > 1): each tile's steps are dealt over `chunks` workgroups, which
+    // leave their sums in `parts` for prefill_fixup_q4k to add in chunk order
+    int chunks;
+    float* parts;  // [tile][chunk][wave][token tile q][register v][lane]
 };
+
+extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
 
 // one group's operands (read from LDS) and products (matrix-core results) for the wave's two
 // token tiles
@@ -135,21 +141,31 @@ __device__ __forceinline__ void stage(const PrefillArgs& a, const StageOffsets& 
     }
 }
 
+// the sums' slice of one (tile, chunk) in `parts`: 2 token tiles x 16 registers x 64 lanes a wave
+constexpr int PF_PART = PF_WAVES * 2 * 16 * 64;
+
+template <int MODE>
+__device__ void pf_finish(const PrefillArgs& a, v16f (&acc)[2], int row0, int tok0, int w, int lane);
+
 template <int MODE>
 __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int r = lane & 31, h = lane >> 5;
 
-    // workgroup id -> tiles: ids on one XCD (id % 8) walk its row tiles' token tiles in turn
-    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    // workgroup id -> (chunk, tiles): ids on one XCD (id % 8) walk its row tiles' token tiles in
+    // turn; a split product repeats that walk once per chunk
+    const int per_chunk = (a.row_tiles + 7) / 8 * 8 * a.token_tiles;
+    const int chunk = blockIdx.x / per_chunk, id = blockIdx.x - chunk * per_chunk;
+    const int xcd = id & 7, local = id >> 3;
     const int tt = local % a.token_tiles, rt = (local / a.token_tiles) * 8 + xcd;
     if (rt >= a.row_tiles) return;
     constexpr int OUT_ROWS = MODE == PF_GLU ? PF_ROWS / 2 : PF_ROWS;
     const int row0 = rt * OUT_ROWS, tok0 = tt * PF_TOKENS;
-    const int steps = a.cols / 256;
-    const uint32_t row_bytes = (uint32_t)steps * PF_BLOCK;
+    const int all_steps = a.cols / 256;
+    // this chunk's steps [first, first + steps): all of them unless the product is split
+    const int first = chunk * all_steps / a.chunks, steps = (chunk + 1) * all_steps / a.chunks - first;
+    const uint32_t row_bytes = (uint32_t)all_steps * PF_BLOCK;
     const uint32_t lds0 = (uint32_t)(uintptr_t)pf_lds;
 
     StageOffsets so;
@@ -167,7 +183,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         so.tg[1] = ((uint32_t)lane & 7u) ^ (uint32_t)(w + PF_WAVES);
     }
     const bool full = row0 + (MODE == PF_GLU ? 64 : 128) <= a.rows;
-    stage<MODE>(a, so, row0, tok0, full, lds0, 0, w);
+    stage<MODE>(a, so, row0, tok0, full, lds0, first, w);
 
     // the lane's LDS offsets within a buffer: its row's weights (of the 128: gate or the first 64
     // rows in waves 0, 1), token r's activations of tile q (chunk c = 2g + h at (xo ^ 32g) +
@@ -188,7 +204,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         wait_loads();                        // this step's direct loads are in LDS
         __syncthreads();                     // ... everyone's; and the other buffer is free
         const uint32_t buf = lds0 + (uint32_t)(step & 1) * PF_BUF;
-        if (step + 1 < steps) stage<MODE>(a, so, row0, tok0, full, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, step + 1, w);
+        if (step + 1 < steps)
+            stage<MODE>(a, so, row0, tok0, full, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, first + step + 1, w);
 
         const uint32_t wl = buf + wo;
         const u32x4 hdr = lds_read<u32x4>(wl);
@@ -258,7 +275,23 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         });
     }
 
-    // lane (r, h) holds row 32w + r of the staged rows for tokens 32q + 8(v / 4) + 4h + v % 4
+    if (a.chunks > 1) {  // a chunk's sums, for the fixup to add (coalesced: register v of 64 lanes at a time)
+        float* dst = a.parts + ((size_t)(rt * a.token_tiles + tt) * a.chunks + chunk) * PF_PART + w * (2 * 16 * 64) + lane;
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) dst[(q * 16 + v) * 64] = acc[q][v];
+        return;
+    }
+    pf_finish<MODE>(a, acc, row0, tok0, w, lane);
+}
+
+// The outputs of one workgroup's tile from its sums acc (lane (r, h) of wave w holding row 32w + r
+// of the staged rows for tokens 32q + 8(v / 4) + 4h + v % 4): the GLU of gate and up, the q8 of
+// those, the residual, the stores. Every wave of the workgroup calls it.
+template <int MODE>
+__device__ void pf_finish(const PrefillArgs& a, v16f (&acc)[2], int row0, int tok0, int w, int lane) {
+    const int r = lane & 31, h = lane >> 5;
     int wave_row = 32 * w + r;
     if (MODE == PF_GLU) {
         // the up waves (2, 3) hand their sums to the gate waves (0, 1) through LDS
@@ -338,14 +371,33 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
         }
 }
 
+// A split product's tiles: the chunks' sums added in chunk order (the same sums whichever
+// workgroup ran first), then the tile's outputs as the main kernel would have written them.
+template <int MODE>
+__global__ __launch_bounds__(64 * PF_WAVES) void prefill_fixup_q4k(PrefillArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int tile = blockIdx.x, rt = tile / a.token_tiles, tt = tile - rt * a.token_tiles;
+    constexpr int OUT_ROWS = MODE == PF_GLU ? PF_ROWS / 2 : PF_ROWS;
+    const float* src = a.parts + (size_t)tile * a.chunks * PF_PART + w * (2 * 16 * 64) + lane;
+    v16f acc[2] = {};
+    for (int c = 0; c < a.chunks; c++, src += PF_PART)
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[q][v] += src[(q * 16 + v) * 64];
+    pf_finish<MODE>(a, acc, rt * OUT_ROWS, tt * PF_TOKENS, w, lane);
+}
+
+// LDS the fixup's epilogue uses: the GLU's exchange of up sums, then 64 tokens' rows for the q8
+constexpr int PF_FIXUP_LDS = 2 * 2 * 16 * 64 * 4 + 64 * 68 * 4;
+
 template <int MODE>
 int prefill_go(PrefillArgs& a, hipStream_t st) {
-    const int out_rows = MODE == PF_GLU ? PF_ROWS / 2 : PF_ROWS;
-    a.row_tiles = (a.rows + out_rows - 1) / out_rows;
-    a.token_tiles = (a.tokens + PF_TOKENS - 1) / PF_TOKENS;
-    // ids cover whole groups of 8 row tiles (one per XCD); ids past the last row tile exit at once
+    // ids cover whole groups of 8 row tiles (one per XCD), once per chunk; ids past the last row
+    // tile exit at once
     const int groups = (a.row_tiles + 7) / 8;
-    const int grid = groups * 8 * a.token_tiles;
+    const int grid = groups * 8 * a.token_tiles * a.chunks;
     static const hipError_t allowed = hipFuncSetAttribute((const void*)prefill_q4k<MODE>,
                                                           hipFuncAttributeMaxDynamicSharedMemorySize, PF_LDS);
     if (allowed != hipSuccess) {
@@ -353,15 +405,33 @@ int prefill_go(PrefillArgs& a, hipStream_t st) {
         return -1;
     }
     hipLaunchKernelGGL((prefill_q4k<MODE>), dim3(grid), dim3(64 * PF_WAVES), PF_LDS, st, a);
-    return check_launch("prefill");
+    if (check_launch("prefill")) return -1;
+    if (a.chunks > 1) {
+        hipLaunchKernelGGL((prefill_fixup_q4k<MODE>), dim3(a.row_tiles * a.token_tiles), dim3(64 * PF_WAVES),
+                           PF_FIXUP_LDS, st, a);
+        return check_launch("prefill fixup");
+    }
+    return 0;
 }
 
 }  // namespace
 
+Split prefill_split(int mode, int rows, int cols, int tokens) {
+    const int out_rows = mode == PF_GLU ? PF_ROWS / 2 : PF_ROWS;
+    const int tiles = (rows + out_rows - 1) / out_rows * ((tokens + PF_TOKENS - 1) / PF_TOKENS);
+    return split_schedule(tiles, cols / 256, (int64_t)PF_PART * 4);
+}
+
 int prefill_launch(int mode, const void* const* ws, int rows, int cols, const int32_t* xq, const float* xd,
                    const float* xs, int tokens, const float* residual, int kind, float* out, hipStream_t st,
-                   uint32_t* hq, float* hd, float* hs) {
+                   uint32_t* hq, float* hd, float* hs, void* workspace, int64_t workspace_bytes) {
     PrefillArgs a = {};
+    const int out_rows = mode == PF_GLU ? PF_ROWS / 2 : PF_ROWS;
+    a.row_tiles = (rows + out_rows - 1) / out_rows;
+    a.token_tiles = (tokens + PF_TOKENS - 1) / PF_TOKENS;
+    const Split sp = prefill_split(mode, rows, cols, tokens);
+    a.chunks = 1;
+    if (sp.chunks > 1 && workspace && workspace_bytes >= sp.bytes) a.chunks = sp.chunks, a.parts = (float*)workspace;
     a.hq = hq, a.hd = hd, a.hs = hs;
     a.w[0] = (const uint8_t*)ws[0];
     a.w[1] = (const uint8_t*)ws[mode == PF_GLU ? 1 : 0];

@@ -63,7 +63,12 @@ struct P6Args {
     const float* residual;
     uint32_t row_bytes;
     int steps, row_tiles, token_tiles;
+    int chunks;    // a split product (chunks > 1): the tile's steps dealt over that many workgroups
+    float* parts;  // [tile][chunk][wave][register v][lane], added by prefill_fixup_q6k
 };
+
+// the sums' slice of one (tile, chunk) in `parts`: 16 registers x 64 lanes a wave
+constexpr int P6_PART = P6_WAVES * 16 * 64;
 
 // the lane's fixed parts of the direct loads
 struct P6Lanes {
@@ -127,6 +132,23 @@ struct P6Res {
     v16i Df, Dh;
 };
 
+// lane (r, h) of wave w holds row row0 + 32 (w % 2) + r for tokens tok0 + 32 (w / 2) + 8(v / 4) + 4h + v % 4
+template <int MODE>
+__device__ __forceinline__ void p6_finish(const P6Args& a, const v16f& acc, int row0, int tok0, int w, int lane) {
+    const int r = lane & 31, h = lane >> 5;
+    const int row = row0 + 32 * (w & 1) + r;
+    if (row >= a.rows) return;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int tok = tok0 + 32 * (w >> 1) + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (tok >= a.tokens) continue;
+        const size_t at = (size_t)tok * a.rows + row;
+        float y = acc[v];
+        if (MODE == PF_RESIDUAL) y += a.residual[at];
+        a.out[at] = y;
+    }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t p6_lds[];
@@ -135,10 +157,15 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
     const int r = lane & 31, h = lane >> 5;
     const int rt = w & 1, tt = w >> 1;  // the wave's row tile and token tile
 
-    // workgroup id -> tiles: ids on one XCD (id % 8) walk its row tiles' token tiles in turn
-    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    // workgroup id -> (chunk, tiles): ids on one XCD (id % 8) walk its row tiles' token tiles in
+    // turn; a split product repeats that walk once per chunk
+    const int per_chunk = (a.row_tiles + 7) / 8 * 8 * a.token_tiles;
+    const int chunk = blockIdx.x / per_chunk, id = blockIdx.x - chunk * per_chunk;
+    const int xcd = id & 7, local = id >> 3;
     const int wt = local % a.token_tiles, wr = (local / a.token_tiles) * 8 + xcd;
     if (wr >= a.row_tiles) return;
+    // this chunk's steps [first, first + steps)
+    const int first = chunk * a.steps / a.chunks, steps = (chunk + 1) * a.steps / a.chunks - first;
     const int row0 = wr * P6_ROWS, tok0 = wt * P6_TOKENS;
     const uint32_t lds0 = (uint32_t)(uintptr_t)p6_lds;
 
@@ -149,7 +176,7 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
     o.tt = (uint32_t)lane >> 3;
     o.tg[0] = ((uint32_t)lane & 7u) ^ (uint32_t)w;
     o.tg[1] = ((uint32_t)lane & 7u) ^ (uint32_t)(w + P6_WAVES);
-    p6_stage(a, o, row0, tok0, lds0, 0, w);
+    p6_stage(a, o, row0, tok0, lds0, first, w);
 
     // the lane's LDS offsets within a buffer: its row's slot (and the lane half's 16 bytes of a
     // 32-byte run), its token's activations (chunk c at xo ^ 32 (c / 2) for c = 2g + h) and xd
@@ -163,11 +190,12 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
     if (threadIdx.x < 64) ((uint32_t*)(p6_lds + P6_ZERO))[threadIdx.x] = 0u;  // before the first barrier
 
     v16f acc = {};
-    for (int step = 0; step < a.steps; step++) {
+    for (int i = 0; i < steps; i++) {
+        const int step = first + i;
         wait_loads();     // this step's direct loads are in LDS
         __syncthreads();  // ... everyone's; and the other buffer is free
-        const uint32_t buf = lds0 + (uint32_t)(step & 1) * P6_BUF;
-        if (step + 1 < a.steps) p6_stage(a, o, row0, tok0, lds0 + (uint32_t)((step + 1) & 1) * P6_BUF, step + 1, w);
+        const uint32_t buf = lds0 + (uint32_t)(i & 1) * P6_BUF;
+        if (i + 1 < steps) p6_stage(a, o, row0, tok0, lds0 + (uint32_t)((i + 1) & 1) * P6_BUF, step + 1, w);
 
         const uint32_t hbuf = h ? buf : lds0 + P6_ZERO;
         const uint32_t lead = 2u * (uint32_t)(step & 1);  // the block's first byte in its window
@@ -237,26 +265,34 @@ __global__ __launch_bounds__(64 * P6_WAVES, 2) void prefill_q6k(P6Args a) {
         });
     }
 
-    // lane (r, h) holds row row0 + 32 rt + r for tokens tok0 + 32 tt + 8(v / 4) + 4h + v % 4
-    const int row = row0 + m;
-    if (row >= a.rows) return;
+    if (a.chunks > 1) {  // a chunk's sums, for the fixup to add
+        float* dst = a.parts + ((size_t)(wr * a.token_tiles + wt) * a.chunks + chunk) * P6_PART + w * (16 * 64) + lane;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int tok = tok0 + 32 * tt + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (tok >= a.tokens) continue;
-        const size_t at = (size_t)tok * a.rows + row;
-        float y = acc[v];
-        if (MODE == PF_RESIDUAL) y += a.residual[at];
-        a.out[at] = y;
+        for (int v = 0; v < 16; v++) dst[v * 64] = acc[v];
+        return;
     }
+    p6_finish<MODE>(a, acc, row0, tok0, w, lane);
+}
+
+// A split product's tiles: the chunks' sums added in chunk order, then the outputs
+template <int MODE>
+__global__ __launch_bounds__(64 * P6_WAVES) void prefill_fixup_q6k(P6Args a) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int tile = blockIdx.x, wr = tile / a.token_tiles, wt = tile - wr * a.token_tiles;
+    const float* src = a.parts + (size_t)tile * a.chunks * P6_PART + w * (16 * 64) + lane;
+    v16f acc = {};
+    for (int c = 0; c < a.chunks; c++, src += P6_PART)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[v] += src[v * 64];
+    p6_finish<MODE>(a, acc, wr * P6_ROWS, wt * P6_TOKENS, w, lane);
 }
 
 template <int MODE>
 int p6_go(P6Args& a, hipStream_t st) {
-    a.row_tiles = (a.rows + P6_ROWS - 1) / P6_ROWS;
-    a.token_tiles = (a.tokens + P6_TOKENS - 1) / P6_TOKENS;
-    // ids cover whole groups of 8 row tiles (one per XCD); ids past the last row tile exit at once
-    const int grid = (a.row_tiles + 7) / 8 * 8 * a.token_tiles;
+    // ids cover whole groups of 8 row tiles (one per XCD), once per chunk; ids past the last row
+    // tile exit at once
+    const int grid = (a.row_tiles + 7) / 8 * 8 * a.token_tiles * a.chunks;
     static const hipError_t allowed =
         hipFuncSetAttribute((const void*)prefill_q6k<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, P6_LDS);
     if (allowed != hipSuccess) {
@@ -264,16 +300,31 @@ int p6_go(P6Args& a, hipStream_t st) {
         return -1;
     }
     hipLaunchKernelGGL((prefill_q6k<MODE>), dim3(grid), dim3(64 * P6_WAVES), P6_LDS, st, a);
-    return check_launch("prefill");
+    if (check_launch("prefill")) return -1;
+    if (a.chunks > 1) {
+        hipLaunchKernelGGL((prefill_fixup_q6k<MODE>), dim3(a.row_tiles * a.token_tiles), dim3(64 * P6_WAVES), 0, st, a);
+        return check_launch("prefill fixup");
+    }
+    return 0;
 }
 
 }  // namespace
 
 bool prefill_q6k_fits(int cols) { return cols > 0 && cols % 512 == 0; }
 
+Split prefill_q6k_split(int rows, int cols, int tokens) {
+    const int tiles = (rows + P6_ROWS - 1) / P6_ROWS * ((tokens + P6_TOKENS - 1) / P6_TOKENS);
+    return split_schedule(tiles, cols / 256, (int64_t)P6_PART * 4);
+}
+
 int prefill_q6k_launch(const void* w, int rows, int cols, const int32_t* xq, const float* xd, int tokens,
-                       const float* residual, float* out, hipStream_t st) {
+                       const float* residual, float* out, hipStream_t st, void* workspace, int64_t workspace_bytes) {
     P6Args a = {};
+    a.row_tiles = (rows + P6_ROWS - 1) / P6_ROWS;
+    a.token_tiles = (tokens + P6_TOKENS - 1) / P6_TOKENS;
+    const Split sp = prefill_q6k_split(rows, cols, tokens);
+    a.chunks = 1;
+    if (sp.chunks > 1 && workspace && workspace_bytes >= sp.bytes) a.chunks = sp.chunks, a.parts = (float*)workspace;
     a.w = (const uint8_t*)w;
     a.out = out;
     a.rows = rows, a.cols = cols, a.tokens = tokens;

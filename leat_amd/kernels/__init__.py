@@ -21,6 +21,8 @@ GROUP = 32  # int8 activations sharing one scale (leat/kernels/common.py:20)
 MATVEC_TOKENS = 8  # the most tokens the decode kernels take (leat/kernels/matvec.py:36)
 FEW_TOKENS = 16  # leat's tile height for short prompts (leat/kernels/matmul.py:54)
 GLU_KINDS = {"silu": 0, "gelu": 1, "oai": 2}
+MAX_USED = 64  # the most experts a token may take on the expert kernels (include/leatmi.h)
+MAX_PAIRS = 65535  # (token, slot) pairs of one expert launch: longer prompts run in chunks of tokens
 
 Norm = tuple[torch.Tensor, float]
 Q8 = tuple[torch.Tensor, torch.Tensor, torch.Tensor]
@@ -40,6 +42,12 @@ def _rows_of(x: torch.Tensor) -> int:
 
 def _f32(x: torch.Tensor) -> torch.Tensor:
     return x.float().contiguous()
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    # t contiguous and 16-byte aligned (a view into a mapped file may be neither)
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _blocks(w: QTensor) -> int:
@@ -73,6 +81,11 @@ def _self_quantized(ggml_type: GGMLType, cols: int, tokens: int) -> bool:
     return False
 
 
+def _aligned16(*ts: torch.Tensor | None) -> bool:
+    # the f32-input kernels read x and the norm weight in 16-byte loads
+    return all(t is None or t.data_ptr() % 16 == 0 for t in ts)
+
+
 def _norm_args(norm: Norm | None) -> tuple[torch.Tensor | None, float]:
     return (None, 0.0) if norm is None else (_f32(norm[0]), float(norm[1]))
 
@@ -90,9 +103,9 @@ def quantize_q8(x: torch.Tensor, norm: Norm | None = None, rows: int | None = No
     word w, and the per-group d and s. Each is one flat tensor, row after row."""
     _lib.require_device(x)
     count, n = x.shape
-    src = _f32(x)
+    src = _aligned(_f32(x))  # the quantizer reads x and the weight in 16-byte loads
     q, d, s = _q8_buffers(count, n, src.device)
-    weight, eps = (None, 0.0) if norm is None else (_f32(norm[0]), float(norm[1]))
+    weight, eps = (None, 0.0) if norm is None else (_aligned(_f32(norm[0])), float(norm[1]))
     done = count if rows is None else int(rows)
     _lib.call("leat_quantize_q8", src.data_ptr(), done, n, _lib.ptr(weight), eps, q.data_ptr(), d.data_ptr(),
               s.data_ptr(), _lib.stream(src.device))  # fmt: skip
@@ -123,10 +136,10 @@ def matvecs(
     outs = [torch.empty(tokens * w.shape[0], dtype=torch.float32, device=device) for w in ws]
     lead = x.shape[:-1]
     one_type = all(w.type == ws[0].type for w in ws) and len(ws) <= 4
-    if one_type and _self_quantized(ws[0].type, cols, tokens):
+    src = _f32(x)
+    weight, eps = _norm_args(norm)
+    if one_type and _self_quantized(ws[0].type, cols, tokens) and _aligned16(src, weight):
         # one launch: each workgroup quantizes x itself (after the norm), then the products
-        src = _f32(x)
-        weight, eps = _norm_args(norm)
         stream = _lib.stream(device)
         if residual is None:
             n = len(ws)
@@ -170,10 +183,10 @@ def _swiglu(x, gate, up, norm, kind, q8_out):
     rows = gate.shape[0]
     device = x.device
     out = torch.empty(tokens * rows, dtype=torch.float32, device=device)
-    if _self_quantized(gate.type, cols, tokens):
+    src = _f32(x)
+    weight, eps = _norm_args(norm)
+    if _self_quantized(gate.type, cols, tokens) and _aligned16(src, weight):
         q8 = _q8_buffers(tokens, rows, device) if q8_out and rows % 32 == 0 else None
-        weight, eps = _norm_args(norm)
-        src = _f32(x)
         hq, hd, hs = (None, None, None) if q8 is None else (t.data_ptr() for t in q8)
         _lib.call("leat_glu_matvec_f32", int(gate.type), _blocks(gate), _blocks(up), rows, cols, src.data_ptr(),
                   tokens, _lib.ptr(weight), eps, GLU_KINDS[kind], out.data_ptr(), hq, hd, hs,
@@ -239,13 +252,22 @@ def supports_matmul(x: torch.Tensor, w: QTensor) -> bool:
     return _single_sequence(x) and matmul_fits(w.type, *w.shape) and _on_gfx950(x)
 
 
+def _workspace(ggml_type: GGMLType, rows: int, cols: int, tokens: int, gated: bool, device) -> tuple[int | None, int]:
+    # (address, bytes) of the workspace a split prefill product takes (matmul.py:1005-1010), or none
+    size = _lib.workspace_bytes(ggml_type, rows, cols, tokens, gated)
+    if size == 0:
+        return None, 0
+    return torch.empty(size, dtype=torch.uint8, device=device).data_ptr(), size
+
+
 def _matmul(w: QTensor, q8: Q8, tokens: int, residual: torch.Tensor | None) -> torch.Tensor:
     xq, xd, xs = q8
     rows, cols = w.shape
     out = torch.empty(tokens * rows, dtype=torch.float32, device=xq.device)
     add = None if residual is None else _f32(residual).reshape(-1)
+    ws, size = _workspace(w.type, rows, cols, tokens, False, xq.device)
     _lib.call("leat_matmul", int(w.type), _blocks(w), rows, cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(),
-              tokens, _lib.ptr(add), out.data_ptr(), _lib.stream(xq.device))  # fmt: skip
+              tokens, _lib.ptr(add), out.data_ptr(), ws, size, _lib.stream(xq.device))  # fmt: skip
     return out
 
 
@@ -284,18 +306,21 @@ def feed_forward(
                   xs.data_ptr(), tokens, _lib.ptr(add), out.data_ptr(), _lib.stream(x.device))  # fmt: skip
         return out.view(*x.shape[:-1], down.shape[0])
     xq, xd, xs = quantize_q8(x.reshape(tokens, cols), norm)
+    ws, size = _workspace(gate.type, rows, cols, tokens, True, x.device)
     if rows % GROUP == 0:  # the GLU writes the down product's q8 input (Q4_K: in its own kernel)
         i32, f32 = dict(dtype=torch.int32, device=x.device), dict(dtype=torch.float32, device=x.device)
         hq8 = (torch.empty(tokens * rows // 4, **i32), torch.empty(tokens * rows // GROUP, **f32),
                torch.empty(tokens * rows // GROUP, **f32))  # fmt: skip
-        hidden = None if gate.type == GGMLType.Q4_K else torch.empty(tokens, rows, **f32)
+        # the f32 outputs, which Q4_K's prefill kernel can skip past FEW_TOKENS
+        keep = gate.type != GGMLType.Q4_K or tokens <= FEW_TOKENS
+        hidden = torch.empty(tokens, rows, **f32) if keep else None
         _lib.call("leat_glu_matmul_q8", int(gate.type), _blocks(gate), _blocks(up), rows, cols, xq.data_ptr(),
                   xd.data_ptr(), xs.data_ptr(), tokens, GLU_KINDS[kind], _lib.ptr(hidden), hq8[0].data_ptr(),
-                  hq8[1].data_ptr(), hq8[2].data_ptr(), _lib.stream(x.device))  # fmt: skip
+                  hq8[1].data_ptr(), hq8[2].data_ptr(), ws, size, _lib.stream(x.device))  # fmt: skip
     else:
         hidden = torch.empty(tokens, rows, dtype=torch.float32, device=x.device)
         _lib.call("leat_glu_matmul", int(gate.type), _blocks(gate), _blocks(up), rows, cols, xq.data_ptr(),
-                  xd.data_ptr(), xs.data_ptr(), tokens, GLU_KINDS[kind], hidden.data_ptr(),
+                  xd.data_ptr(), xs.data_ptr(), tokens, GLU_KINDS[kind], hidden.data_ptr(), ws, size,
                   _lib.stream(x.device))  # fmt: skip
         hq8 = quantize_q8(hidden)
     out = _matmul(down, hq8, tokens, x if residual else None)
@@ -324,12 +349,6 @@ def supports_scores(x: torch.Tensor, router: QTensor) -> bool:
     """An F32 router whose rows are whole 16-byte loads (leat/kernels/experts.py:110-112), on a
     gfx950 GPU."""
     return router.type == GGMLType.F32 and router.shape[1] % 4 == 0 and _on_gfx950(x)
-
-
-def _aligned(t: torch.Tensor) -> torch.Tensor:
-    # t contiguous and 16-byte aligned (a view into a mapped file may be neither)
-    t = t.contiguous()
-    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def scores(x: torch.Tensor, norm: Norm, router: QTensor) -> torch.Tensor:
@@ -371,6 +390,7 @@ def supports_mixture(x: torch.Tensor, gate: QTensor, up: QTensor | None, down: Q
     return _single_sequence(x) and _on_gfx950(x)
 
 
+
 def _fused_mixture_fits(ggml_type: int, cols: int, rows: int, experts: int, used: int, tokens: int) -> bool:
     """Whether leat_experts_glu_f32 takes the decode mixture's first steps in one launch
     (include/leatmi.h): 1..8 tokens, hidden rows in 32s, rows of at most 4 turns of a wave's
@@ -408,9 +428,20 @@ def mixture(
     With up None, gate stacks each expert's gate rows, then its up rows. Tokens past the first
     `live` are batch padding: no expert runs for them and their mixture is 0."""
     _, tokens, dim = x.shape
+    if not 0 < used <= MAX_USED:
+        raise _lib.LeatError(f"mixture: {used} experts a token (the kernels take 1..{MAX_USED})")
+    real = tokens if live is None else int(live)
+    chunk = MAX_PAIRS // used
+    if real > chunk:  # a long prompt: the expert launches take at most MAX_PAIRS pairs each
+        out = torch.cat([
+            mixture(x[:, at : min(at + chunk, real)], scores.reshape(1, tokens, -1)[:, at : min(at + chunk, real)], gate,
+                    up, down, used, norm, kind, scales, residual, biases)
+            for at in range(0, real, chunk)
+        ] + ([x[:, real:].float() if residual else torch.zeros_like(x[:, real:], dtype=torch.float32)]
+             if real < tokens else []), dim=1)  # fmt: skip
+        return out
     device = x.device
     rows = down.shape[2]
-    real = tokens if live is None else int(live)
     flat_x = _f32(x.reshape(tokens, dim))
     out = flat_x.clone() if residual else torch.zeros_like(flat_x)
     if real == 0:
@@ -420,13 +451,14 @@ def mixture(
     gate_b, up_b, down_b = (None, None, None) if biases is None else (_f32(b).reshape(-1) for b in biases)
     stream = _lib.stream(device)
     route_scores = _f32(scores.reshape(tokens, -1)[:real])
-    if _fused_mixture_fits(gate.type, dim, rows, experts, used, real) and flat_x.data_ptr() % 16 == 0:
+    norm_w, eps = _norm_args(norm)
+    aligned = flat_x.data_ptr() % 16 == 0 and (norm_w is None or norm_w.data_ptr() % 16 == 0)
+    if _fused_mixture_fits(gate.type, dim, rows, experts, used, real) and aligned:
         # decode: routing, norm + quantize, the experts' gate+up+GLU and the quantized hidden rows
         # in one launch
         ids = torch.empty(pairs, dtype=torch.int32, device=device)
         weights = torch.empty(pairs, dtype=torch.float32, device=device)
         hq, hd, hs = _q8_buffers(pairs, rows, device)
-        norm_w, eps = _norm_args(norm)
         _lib.call("leat_experts_glu_f32", int(gate.type), _blocks(gate), None if up is None else _blocks(up), experts,
                   rows, dim, flat_x.data_ptr(), real, _lib.ptr(norm_w), eps, route_scores.data_ptr(), used,
                   _lib.ptr(gate_b), _lib.ptr(up_b), GLU_KINDS[kind], ids.data_ptr(), weights.data_ptr(), None,
@@ -447,7 +479,7 @@ def mixture(
 
 
 __all__ = [
-    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
+    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
     "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
     "supports_mixture", "supports_scores", "swiglu",
 ]  # fmt: skip

@@ -124,7 +124,7 @@ def mixture(
     then its up rows. On the kernels, tokens past the first `live` are batch padding: they read
     no experts and their mixture is zero. The reference semantics compute them like any other
     token."""
-    if not reference_mode() and kernels.supports_mixture(x, gate, up, down):
+    if not reference_mode() and used <= kernels.MAX_USED and kernels.supports_mixture(x, gate, up, down):
         return kernels.mixture(x, scores, gate, up, down, used, norm, kind, scales, residual, biases, live)
     dim = x.shape[-1]
     normed = rms_norm(x.float(), *norm).reshape(-1, dim)

@@ -140,7 +140,7 @@ def test_prefill_glu_q8_bench_shape(cuda):
     hd, hs = (torch.empty(tokens * rows // 32, dtype=torch.float32, device=cuda) for _ in range(2))
     _lib.call("leat_glu_matmul_q8", int(Q4_K), gate.q.data.data_ptr(), up.q.data.data_ptr(), rows, cols,
               xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), tokens, 0, out.data_ptr(), hq.data_ptr(), hd.data_ptr(),
-              hs.data_ptr(), _lib.stream())  # fmt: skip
+              hs.data_ptr(), None, 0, _lib.stream())  # fmt: skip
     got = host(out).reshape(tokens, rows)
     q, d, _ = O.quantize_q8(x)
     xo = _dense_q8(q, d, cols)
