@@ -134,6 +134,15 @@ int leat_matmul(int type, const void *w, int rows, int cols, const int32_t *xq, 
                 const float *xs, int tokens, const float *residual, float *out, void *workspace,
                 int64_t workspace_bytes, void *stream);
 
+/* No counterpart in leat: leat_matmul for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). A split product's partial sums go to
+ * a file-scope device array of 8 MiB on each GPU instead of a caller workspace; products whose
+ * split needs more (leat_matmul_workspace) return -1. Calls on one GPU share its array: calls that
+ * overlap on one GPU race, calls in one stream order do not. Allocates nothing. */
+int leat_matmul_noalloc(int type, const void *w, int rows, int cols, const int32_t *xq,
+                        const float *xd, const float *xs, int tokens, const float *residual,
+                        float *out, void *stream);
+
 /* Replaces the gated product of leat/kernels/matmul.py:1069-1081 feed_forward() (_products with
  * gated=True): out[t * rows + r] = glu(kind)(gate[r] . x[t], up[r] . x[t]), gate and up in one
  * kernel. Same shape, tile and workspace rules as leat_matmul. */

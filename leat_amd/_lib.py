@@ -29,6 +29,7 @@ SIGNATURES: dict[str, list] = {
     "leat_group_dots": [_i, _p, _i, _i, _p, _i, _p, _p],
     "leat_matmul_workspace": [_i, _i, _i, _i, _i],
     "leat_matmul": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p, _i64, _p],
+    "leat_matmul_noalloc": [_i, _p, _i, _i, _p, _p, _p, _i, _p, _p, _p],
     "leat_glu_matmul": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _i64, _p],
     "leat_route": [_p, _i, _i, _i, _p, _p, _p],
     "leat_scores": [_p, _i, _i, _p, _f, _p, _i, _p, _p],

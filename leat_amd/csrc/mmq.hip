@@ -393,6 +393,11 @@ static int64_t workspace_of(int type, int rows, int cols, int tokens, bool gated
     return 0;
 }
 
+int64_t matmul_workspace(int type, int rows, int cols, int tokens, bool gated) {
+    if (rows <= 0 || cols <= 0 || tokens <= 0 || cols % 256 != 0) return 0;
+    return workspace_of(type, rows, cols, tokens, gated);
+}
+
 int matmul_go(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd, const float* xs,
               int tokens, const float* residual, float* out, void* workspace, int64_t workspace_bytes, hipStream_t st) {
     if (mmq_check(type, w, rows, cols, xq, xd, xs, tokens, out)) return -1;
@@ -418,8 +423,7 @@ int matmul_go(int type, const void* w, int rows, int cols, const int32_t* xq, co
 using namespace leat;
 
 extern "C" int64_t leat_matmul_workspace(int type, int rows, int cols, int tokens, int gated) {
-    if (rows <= 0 || cols <= 0 || tokens <= 0 || cols % 256 != 0) return 0;
-    return workspace_of(type, rows, cols, tokens, gated != 0);
+    return matmul_workspace(type, rows, cols, tokens, gated != 0);
 }
 
 extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd,

@@ -22,6 +22,11 @@ Split split_schedule(int tiles, int steps, int64_t part_bytes);
 // the current device's compute units
 int cu_count();
 
+// leat_matmul (mmq.hip) with an explicit workspace, and the workspace its split takes
+int64_t matmul_workspace(int type, int rows, int cols, int tokens, bool gated);
+int matmul_go(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd, const float* xs,
+              int tokens, const float* residual, float* out, void* workspace, int64_t workspace_bytes, hipStream_t st);
+
 // Q4_K weights, 16-byte aligned, cols a multiple of 256, xq 16-byte aligned (checked by the caller).
 // mode: 0 plain, 1 residual, 2 GLU (ws[0] gate, ws[1] up; out may be null when hq is given). hq,
 // hd, hs (the GLU, rows a multiple of 32): also the q8 of the outputs, as quantize_q8 gives it.
