@@ -211,6 +211,49 @@ int leat_experts_down(int type, const void *w, int experts, int rows, int cols, 
                       int tokens, int used, const float *scales, const float *bias,
                       const float *residual, float *out, void *stream);
 
+/* ---------------------------------------------------------------- the decode step around them */
+
+/* Replaces leat/ops.py:166-178 embedding(tokens, w): out[t, :] = row ids[t] of W decoded to f32 as
+ * leat_dequantize decodes it (ids outside 0..rows-1 give zeros). ids is a device array. */
+int leat_embedding(int type, const void *w, int rows, int cols, const int32_t *ids, int tokens,
+                   float *out, void *stream);
+
+/* Replaces leat/kernels/attention.py:656-782 rotate() for heads without biases or norms: each
+ * token's q (tokens, heads, dim) and k (tokens, kv_heads, dim) turned by RoPE over the first
+ * `rotated` dimensions (pairs of adjacent dimensions, or with `halves` dimensions i and
+ * i + rotated / 2), by the angles of the token's position in cos and sin (cache_positions,
+ * rotated / 2) f32; q to q_out (heads, tokens, dim) f32, and k with v (tokens, kv_heads, dim)
+ * stored as f16 in the cache (2, cache_slots, kv_heads, cache_positions, dim) at the token's
+ * slot and position. slots and positions are device arrays; a token whose slot or position
+ * lies outside the cache stores nothing. */
+int leat_rotate(const float *q, const float *k, const float *v, int tokens, int heads, int kv_heads,
+                int dim, const float *cos, const float *sin, int rotated, int halves,
+                const int32_t *slots, const int32_t *positions, float *q_out, void *cache,
+                int cache_slots, int cache_positions, void *stream);
+
+/* The workspace bytes leat_attention needs for `rows` rows of `heads` heads and rows of at most
+ * max_length keys. */
+int64_t leat_attention_workspace(int rows, int heads, int max_length);
+
+/* Replaces leat/kernels/attention.py:226-279 attention() (FlashDecoding): for each row (a query
+ * token), out[row, h * dim ..] = softmax over keys 0 .. lengths[row] - 1 of slot slots[row] of
+ * (q[h, row] . key * scale) times the values, kv head h / (heads / kv_heads); q (heads, rows, dim)
+ * f32 as leat_rotate writes it, the f16 cache as leat_rotate fills it, out (rows, heads * dim)
+ * f32. Scores, weights and sums in f32. dim 128; 1, 2, 4 or 8 query heads a kv head; slots and
+ * lengths device arrays, every length at most max_length (which sizes the launch). */
+int leat_attention(const float *q, const void *cache, int cache_slots, int kv_heads,
+                   int cache_positions, int dim, int rows, int heads, const int32_t *slots,
+                   const int32_t *lengths, int max_length, float scale, float *workspace,
+                   int64_t workspace_bytes, float *out, void *stream);
+
+/* The workspace bytes leat_argmax needs for `rows` rows. */
+int64_t leat_argmax_workspace(int rows);
+
+/* Replaces leat/kernels/argmax.py:14-59 argmax(x): out[row] = the index of the largest value of
+ * row `row` of x (rows, n) f32, the lowest index among equal values; NaN is never chosen. */
+int leat_argmax(const float *x, int rows, int n, void *workspace, int64_t workspace_bytes,
+                int32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

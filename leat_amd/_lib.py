@@ -40,6 +40,12 @@ SIGNATURES: dict[str, list] = {
     "leat_matvec_f32": [_i, _p, _i, _i, _p, _i, _p, _f, _p, _p, _p],
     "leat_glu_matvec_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p],
     "leat_glu_matmul_q8": [_i, _p, _p, _i, _i, _p, _p, _p, _i, _i, _p, _p, _p, _p, _p, _i64, _p],
+    "leat_embedding": [_i, _p, _i, _i, _p, _i, _p, _p],
+    "leat_rotate": [_p, _p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _p, _p, _p, _p, _i, _i, _p],
+    "leat_attention_workspace": [_i, _i, _i],
+    "leat_attention": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i, _f, _p, _i64, _p, _p],
+    "leat_argmax_workspace": [_i],
+    "leat_argmax": [_p, _i, _i, _p, _i64, _p, _p],
     "leat_glu_matvec_f32": [_i, _p, _p, _i, _i, _p, _i, _p, _f, _i, _p, _p, _p, _p, _p],
 }
 
@@ -61,7 +67,8 @@ def lib() -> ctypes.CDLL:
     handle.leat_last_error.restype = ctypes.c_char_p
     handle.leat_target.restype = ctypes.c_char_p
     handle.leat_abi_version.restype = ctypes.c_int
-    handle.leat_matmul_workspace.restype = ctypes.c_int64
+    for name in ("leat_matmul_workspace", "leat_attention_workspace", "leat_argmax_workspace"):
+        getattr(handle, name).restype = ctypes.c_int64
     return handle
 
 

@@ -71,6 +71,28 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
     for (int l = 0; l < 32; l += 4) *(float4*)(o + l) = make_float4(y[l], y[l + 1], y[l + 2], y[l + 3]);
 }
 
+// out[t, :] = row ids[t] of W decoded (ids outside the matrix give zeros): a thread per 32 weights
+template <int TYPE>
+__global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, int rows, int cols,
+                                                        const int32_t* __restrict__ ids, float* __restrict__ out) {
+    constexpr int PER = block_weights<TYPE>() / 32;
+    const int t = blockIdx.y, pieces = cols / 32;
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= pieces) return;
+    const int id = ids[t];
+    float y[32];
+    if (id >= 0 && id < rows) {
+        const int64_t nb = cols / block_weights<TYPE>();
+        dequant_piece<TYPE>(w + ((int64_t)id * nb + p / PER) * block_bytes<TYPE>(), p % PER, y);
+    } else {
+#pragma unroll
+        for (int l = 0; l < 32; l++) y[l] = 0.0f;
+    }
+    float* o = out + (int64_t)t * cols + (int64_t)p * 32;
+#pragma unroll
+    for (int l = 0; l < 32; l += 4) *(float4*)(o + l) = make_float4(y[l], y[l + 1], y[l + 2], y[l + 3]);
+}
+
 // out[t * rows + row] = sum_c x[t, c] * W[row, c] (+ residual): one wave per row, lanes over
 // pieces of 32 weights, each decoded exactly as above then multiplied into f32 sums
 template <int TYPE, int B>
@@ -179,6 +201,23 @@ extern "C" int leat_dequantize(int type, const void* blocks, int64_t n_blocks, f
     default: set_error("dequantize: unsupported type %d", type); return -1;
     }
     return check_launch("dequantize");
+}
+
+extern "C" int leat_embedding(int type, const void* w, int rows, int cols, const int32_t* ids, int tokens, float* out,
+                              void* stream) {
+    LEAT_REQUIRE(w && ids && out && rows > 0, "embedding: null pointer or empty matrix");
+    LEAT_REQUIRE(tokens >= 0 && tokens <= 65535, "embedding: %d tokens", tokens);
+    if (check_cols(type, cols)) return -1;
+    if (tokens == 0) return 0;
+    const dim3 grid((cols / 32 + 255) / 256, tokens);
+    hipStream_t st = (hipStream_t)stream;
+    const uint8_t* b = (const uint8_t*)w;
+    switch (type) {
+    case Q8_0: hipLaunchKernelGGL(embedding_kernel<Q8_0>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
+    case Q4_K: hipLaunchKernelGGL(embedding_kernel<Q4_K>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
+    default: hipLaunchKernelGGL(embedding_kernel<Q6_K>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
+    }
+    return check_launch("embedding");
 }
 
 template <int TYPE>

@@ -15,6 +15,16 @@ import ctypes
 import torch
 
 from leat_amd import _lib
+from leat_amd.kernels.attention import (
+    argmax,
+    attention,
+    embedding,
+    rotate,
+    supports_argmax,
+    supports_attention,
+    supports_embedding,
+    supports_rotate,
+)
 from leat_amd.quant import BLOCK, KERNEL_TYPES, GGMLType, QTensor
 
 GROUP = 32  # int8 activations sharing one scale (leat/kernels/common.py:20)
@@ -479,6 +489,8 @@ def mixture(
 
 
 __all__ = [
+    "argmax", "attention", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
+    "supports_rotate",
     "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
     "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
     "supports_mixture", "supports_scores", "swiglu",

@@ -1,0 +1,225 @@
+"""A Llama-architecture decoder on this library's kernels: the part of leat's model
+(leat/model.py:370-423, 497-558) a Llama 3.1 8B decode step runs.
+
+Per step and row (one token of one sequence each): the token's embedding; per layer RMSNorm and
+q/k/v in one launch that quantizes its own input, RoPE with the keys and values stored in an f16
+cache, FlashDecoding over the row's slot, o plus the residual, the feed-forward block (norm, gate
+and up with SiLU in one launch writing the down product's int8 input, down plus the residual);
+the final norm and the Q6_K output head in one launch; the greedy next token. Every launch takes
+device buffers and device slots and positions, so a step is captured once as a HIP graph and
+replayed (leat/engine.py:784-806 captures its steps the same way with TinyJit).
+
+Weights are GGUF blocks as stored (QTensor); `synthetic` draws a random-init model of a given
+shape in Q4_K_M (Q4_K matrices, Q6_K down and output) with the benchmark's distributions.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from leat_amd import kernels, ops
+from leat_amd.quant import BLOCK, GGMLType, QTensor
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    """The sizes of a Llama-architecture model (leat/model.py's Config for arch "llama")."""
+
+    dim: int = 4096
+    layers: int = 32
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 14336
+    vocab: int = 128256
+    norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    # Llama 3.1's frequency scaling (factor, low and high frequency factors, original context),
+    # which GGUF files carry as rope_freqs.weight; None for plain RoPE
+    rope_scaling: tuple[float, float, float, int] | None = (8.0, 1.0, 4.0, 8192)
+    context: int = 4096  # cache positions per slot
+    slots: int = 1  # sequences the cache holds
+
+
+LLAMA3_8B = LlamaConfig()
+
+
+def llama3_rope_factors(dims: int, theta: float, scaling: tuple[float, float, float, int]) -> list[float]:
+    """What divides each RoPE frequency under Llama 3.1's scaling, as its GGUF's rope_freqs holds
+    (Meta's published rule): wavelengths below original / high stay (1), above original / low
+    are scaled by `factor`, and between them the two blend linearly in original / wavelength."""
+    factor, low, high, original = scaling
+    out = []
+    for i in range(dims // 2):
+        wavelength = 2 * math.pi * theta ** (2 * i / dims)  # of frequency theta^(-2i/d)
+        if wavelength < original / high:
+            out.append(1.0)
+        elif wavelength > original / low:
+            out.append(factor)
+        else:
+            smooth = (original / wavelength - low) / (high - low)
+            out.append(1.0 / ((1 - smooth) / factor + smooth))
+    return out
+
+
+def rope_table(dims: int, theta: float, length: int, factors: list[float] | None, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos and sin (length, dims / 2) f32 of angle pos * theta^(-2i/d) / factor_i, the angle in f32
+    as leat computes it (leat/model.py:688-723, plain RoPE without YaRN), cos and sin of that f32
+    angle rounded to f32."""
+    freqs = torch.tensor([theta ** (-2 * i / dims) for i in range(dims // 2)], dtype=torch.float32)
+    angles = torch.arange(length, dtype=torch.float32).unsqueeze(1) * freqs.unsqueeze(0)
+    if factors is not None:
+        angles = angles / torch.tensor(factors, dtype=torch.float32).unsqueeze(0)
+    wide = angles.double()
+    return torch.cos(wide).float().to(device), torch.sin(wide).float().to(device)
+
+
+@dataclass
+class Layer:
+    attn_norm: torch.Tensor
+    q: QTensor
+    k: QTensor
+    v: QTensor
+    o: QTensor
+    ffn_norm: torch.Tensor
+    gate: QTensor
+    up: QTensor
+    down: QTensor
+
+
+@dataclass
+class Weights:
+    embed: QTensor
+    layers: list[Layer]
+    output_norm: torch.Tensor
+    output: QTensor
+
+
+def _synthetic_blocks(ggml_type: GGMLType, rows: int, cols: int, gen: torch.Generator, device) -> QTensor:
+    # uniform bytes, then Q4_K d = f16(|N| * 0.002), dmin = f16(|N| * 0.001); Q6_K d = f16(|N| * 0.002)
+    elements, size = BLOCK[ggml_type]
+    n = rows * cols // elements
+    blocks = torch.randint(0, 256, (n, size), dtype=torch.uint8, device=device, generator=gen)
+
+    def f16(scale: float) -> torch.Tensor:
+        return (torch.randn(n, device=device, generator=gen).abs() * scale).half().view(torch.uint8).view(n, 2)
+
+    if ggml_type == GGMLType.Q4_K:
+        blocks[:, 0:2] = f16(0.002)
+        blocks[:, 2:4] = f16(0.001)
+    elif ggml_type == GGMLType.Q6_K:
+        blocks[:, 208:210] = f16(0.002)
+    else:
+        raise NotImplementedError(ggml_type)
+    return QTensor(blocks, ggml_type, (rows, cols))
+
+
+def synthetic(config: LlamaConfig, seed: int = 0, device="cuda") -> Weights:
+    """A random-init model of `config` in Q4_K_M: Q4_K embedding, attention and gate/up, Q6_K down
+    and output head, norm weights uniform in [0.5, 1.5)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    c, q4, q6 = config, GGMLType.Q4_K, GGMLType.Q6_K
+
+    def norm() -> torch.Tensor:
+        return torch.rand(c.dim, generator=gen, device=device) + 0.5
+
+    layers = [
+        Layer(norm(), _synthetic_blocks(q4, c.heads * c.head_dim, c.dim, gen, device),
+              _synthetic_blocks(q4, c.kv_heads * c.head_dim, c.dim, gen, device),
+              _synthetic_blocks(q4, c.kv_heads * c.head_dim, c.dim, gen, device),
+              _synthetic_blocks(q4, c.dim, c.heads * c.head_dim, gen, device), norm(),
+              _synthetic_blocks(q4, c.ffn, c.dim, gen, device), _synthetic_blocks(q4, c.ffn, c.dim, gen, device),
+              _synthetic_blocks(q6, c.dim, c.ffn, gen, device))
+        for _ in range(c.layers)
+    ]  # fmt: skip
+    embed = _synthetic_blocks(q4, c.vocab, c.dim, gen, device)
+    return Weights(embed, layers, norm(), _synthetic_blocks(q6, c.vocab, c.dim, gen, device))
+
+
+def weight_bytes(w: Weights) -> int:
+    """The bytes of matrices a decode step streams: every layer's, and the output head."""
+    per_layer = sum(m.nbytes for layer in w.layers for m in (layer.q, layer.k, layer.v, layer.o, layer.gate, layer.up, layer.down))
+    return per_layer + w.output.nbytes
+
+
+@dataclass
+class Model:
+    """A decoder with its f16 KV cache (one (2, slots, kv_heads, context, head_dim) tensor per
+    layer) and RoPE tables."""
+
+    config: LlamaConfig
+    weights: Weights
+    cache: list[torch.Tensor] = field(default_factory=list)
+    rope: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def __post_init__(self):
+        c = self.config
+        device = self.weights.output.data.device
+        if not self.cache:
+            self.cache = [torch.zeros(2, c.slots, c.kv_heads, c.context, c.head_dim, dtype=torch.float16, device=device)
+                          for _ in range(c.layers)]  # fmt: skip
+        if self.rope is None:
+            factors = None if c.rope_scaling is None else llama3_rope_factors(c.head_dim, c.rope_theta, c.rope_scaling)
+            self.rope = rope_table(c.head_dim, c.rope_theta, c.context, factors, device)
+
+    def logits(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
+               lengths: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+        """One decode step of `tokens` (B,) int32, row b the token of the sequence in cache slot
+        slots[b] at position positions[b] (device tensors): the logits (B, vocab) f32. Row b's
+        keys and values go to its slot at its position, and it attends over positions
+        0..positions[b] (lengths, positions + 1, may be given to save the addition)."""
+        c, w = self.config, self.weights
+        B = tokens.shape[0]
+        if lengths is None:
+            lengths = positions + 1
+        x = ops.embedding(tokens, w.embed).view(1, B, c.dim)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        rope = (self.rope, c.head_dim)
+        for layer, cache in zip(w.layers, self.cache, strict=True):
+            q, k, v = ops.linears(x, layer.q, layer.k, layer.v, norm=(layer.attn_norm, c.norm_eps))
+            q_rot, _ = ops.rotate(q.view(1, B, c.heads, c.head_dim), k.view(1, B, c.kv_heads, c.head_dim),
+                                  v.view(1, B, c.kv_heads, c.head_dim), cache, None, rope, False, slots, positions)  # fmt: skip
+            att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context)
+            x = ops.linear(att, layer.o, residual=x)
+            x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))
+        (logits,) = ops.linears(x, w.output, norm=(w.output_norm, c.norm_eps))
+        return logits.view(B, c.vocab)
+
+    def step(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
+             lengths: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+        """The greedy next token of each row: argmax of logits(), (B,) int32."""
+        return ops.argmax(self.logits(tokens, slots, positions, lengths)).view(-1)
+
+
+class GraphStep:
+    """A decode step of B rows captured once as a HIP graph over static device buffers `tokens`,
+    `slots` and `positions` (B,) int32; replay() runs it on whatever the buffers hold and leaves
+    the next tokens in `next`. With `advance`, the graph also moves each row on: tokens = next,
+    positions += 1, so replays decode one token after another with no host work between them."""
+
+    def __init__(self, model: Model, batch: int, advance: bool = True):
+        device = model.weights.output.data.device
+        self.model, self.batch = model, batch
+        self.tokens = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.slots = torch.arange(batch, dtype=torch.int32, device=device)
+        self.positions = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.lengths = torch.ones(batch, dtype=torch.int32, device=device)
+        self._run(advance=False)  # once eagerly: every launch checked, and the memory pool warmed
+        torch.cuda.synchronize(device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.next = self._run(advance)
+
+    def _run(self, advance: bool) -> torch.Tensor:
+        torch.add(self.positions, 1, out=self.lengths)
+        nxt = self.model.step(self.tokens, self.slots, self.positions, self.lengths)
+        if advance:
+            self.tokens.copy_(nxt)
+            self.positions.add_(1)
+        return nxt
+
+    def replay(self) -> None:
+        self.graph.replay()

@@ -1,5 +1,6 @@
 """leat's operators on quantized weights (leat/ops.py:18-182) for torch-ROCm tensors: linear,
-linears, feed_forward, router, mixture, glu and rms_norm, with the LEAT_KERNELS=ref switch.
+linears, feed_forward, router, mixture, glu and rms_norm, and the decode step's embedding, rotate,
+attention and argmax (leat/ops.py:166-376, 496-500), with the LEAT_KERNELS=ref switch.
 
 Every product goes one of three ways, chosen per call by `_plan`:
 - "decode": up to kernels.MATVEC_TOKENS tokens, on the matrix-vector kernels;
@@ -12,7 +13,9 @@ Every product goes one of three ways, chosen per call by `_plan`:
 
 from __future__ import annotations
 
+import math
 import os
+from dataclasses import dataclass
 
 import torch
 
@@ -185,3 +188,111 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.
     """x / sqrt(mean(x^2) + eps) over the last axis, times `weight` if given (leat/ops.py:180-182)."""
     scaled = x * torch.rsqrt(torch.mean(x * x, dim=-1, keepdim=True) + eps)
     return scaled if weight is None else scaled * weight
+
+
+# ------------------------------------------------------------------ the decode step around them
+
+
+def embedding(tokens: torch.Tensor, w: QTensor) -> torch.Tensor:
+    """The rows of w (vocab, dim) of token ids, decoded: (…, dim) f32 (leat/ops.py:166-178)."""
+    if not reference_mode() and kernels.supports_embedding(w):
+        return kernels.embedding(tokens, w)
+    vocab, dim = w.shape
+    ids = tokens.reshape(-1).long().to(w.data.device)
+    if w.type in NATIVE:
+        return w.data.reshape(vocab, dim)[ids].float().view(*tokens.shape, dim)
+    rows = w.data.reshape(vocab, -1)[ids].reshape(-1, w.data.shape[-1]).contiguous()
+    return QTensor(rows, w.type, (ids.numel(), dim)).dequant().view(*tokens.shape, dim)
+
+
+@dataclass(frozen=True)
+class Span:
+    """`length` consecutive tokens of one sequence from position `start` of cache slot `slot`
+    (leat/ops.py:201-209). The kernels here take spans of one token: a decode step's rows."""
+
+    slot: int
+    start: int
+    length: int = 1
+
+
+def _span_rows(spans: list[Span]) -> tuple[list[int], list[int]]:
+    # each token's slot and position
+    rows = [(s.slot, s.start + i) for s in spans for i in range(s.length)]
+    return [r[0] for r in rows], [r[1] for r in rows]
+
+
+def rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, halves: bool) -> torch.Tensor:
+    """The first R dimensions of x (B, H, T, D) turned by RoPE, adjacent pairs or with `halves`
+    dimensions i and i + R/2; cos, sin (T, R/2) (leat/ops.py:185-198)."""
+    rotated = 2 * cos.shape[-1]
+    x, rest = x[..., :rotated], x[..., rotated:]
+    if halves:
+        x0, x1 = x.chunk(2, dim=-1)
+        out = torch.cat([x0 * cos - x1 * sin, x0 * sin + x1 * cos], dim=-1)
+    else:
+        pairs = x.reshape(*x.shape[:-1], -1, 2)
+        x0, x1 = pairs[..., 0], pairs[..., 1]
+        out = torch.stack([x0 * cos - x1 * sin, x0 * sin + x1 * cos], dim=-1).flatten(-2)
+    return out if rest.shape[-1] == 0 else torch.cat([out, rest], dim=-1)
+
+
+def rotate(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cache: torch.Tensor, spans: list[Span] | None,
+    rope: tuple[tuple[torch.Tensor, torch.Tensor], int] | None, halves: bool, slots=None, positions=None,
+) -> tuple[torch.Tensor, torch.Tensor]:  # fmt: skip
+    """q (1, T, H, D), k and v (1, T, KV_H, D), the spans' tokens in turn: the first R dimensions of
+    q and k turned by RoPE at the tokens' positions, k and v stored in their slots of the f16 cache
+    (2, slots, KV_H, positions, D) (leat/ops.py:212-276). `slots` and `positions` (device tensors,
+    a token each) may replace the spans, as a captured decode step passes them. Returns q
+    (1, H, T, D) f32 and the cache."""
+    if slots is None:
+        slots, positions = _span_rows(spans)
+    if not reference_mode() and kernels.supports_rotate(q, cache):
+        return kernels.rotate(q, k, v, cache, slots, positions, rope, halves)
+    # the reference semantics token by token, in f32 torch ops
+    slot_list = slots.tolist() if isinstance(slots, torch.Tensor) else list(slots)
+    pos_list = positions.tolist() if isinstance(positions, torch.Tensor) else list(positions)
+    q, k, v = (t.float() for t in (q, k, v))
+    outs = []
+    for t, (slot, pos) in enumerate(zip(slot_list, pos_list, strict=True)):
+        qt, kt = q[:, t : t + 1].transpose(1, 2), k[:, t : t + 1].transpose(1, 2)
+        if rope is not None:
+            cos, sin = (table[pos : pos + 1].float() for table in rope[0])
+            qt, kt = rotary(qt, cos, sin, halves), rotary(kt, cos, sin, halves)
+        cache[0, slot, :, pos] = kt[0, :, 0].to(cache.dtype)
+        cache[1, slot, :, pos] = v[0, t].to(cache.dtype)
+        outs.append(qt)
+    return torch.cat(outs, dim=2), cache
+
+
+def attention(
+    q: torch.Tensor, cache: torch.Tensor, spans: list[Span] | None, scale: float, slots=None, lengths=None,
+    max_length: int | None = None,
+) -> torch.Tensor:  # fmt: skip
+    """q (1, H, T, D), the spans' tokens in turn, each token attending causally over its slot's
+    positions up to its own, scores q.k * scale (leat/ops.py:305-339). `slots` and `lengths`
+    (device tensors, a row each) may replace the spans. Returns (1, T, H * D) f32."""
+    if slots is None:
+        slots, positions = _span_rows(spans)
+        lengths = [p + 1 for p in positions]
+    if not reference_mode() and kernels.supports_attention(q, cache):
+        return kernels.attention(q, cache, slots, lengths, scale, max_length)
+    slot_list = slots.tolist() if isinstance(slots, torch.Tensor) else list(slots)
+    length_list = lengths.tolist() if isinstance(lengths, torch.Tensor) else list(lengths)
+    _, heads, _, dim = q.shape
+    group = heads // cache.shape[2]
+    outs = []
+    for t, (slot, length) in enumerate(zip(slot_list, length_list, strict=True)):
+        keys = cache[0, slot, :, :length].float().repeat_interleave(group, dim=0).contiguous()
+        values = cache[1, slot, :, :length].float().repeat_interleave(group, dim=0).contiguous()
+        scores = torch.matmul(q[0, :, t : t + 1].float(), keys.transpose(-1, -2).contiguous()) * scale
+        outs.append(torch.matmul(scores.softmax(-1), values).reshape(1, heads * dim))
+    return torch.stack(outs, dim=1)
+
+
+def argmax(x: torch.Tensor) -> torch.Tensor:
+    """Each row's index of its largest value, the first one among equal values: (B, V) -> (B, 1)
+    int32 (leat/ops.py:496-500)."""
+    if not reference_mode() and kernels.supports_argmax(x):
+        return kernels.argmax(x)
+    return x.float().nan_to_num(nan=-math.inf).argmax(-1, keepdim=True).to(torch.int32)
