@@ -1,30 +1,35 @@
 """Benchmark: weight-stream GB/s (% of HBM peak) and decode tok/s of the quantized-weight path,
-Llama-3-8B Q4_K_M layer shapes, B = 1 (the headline value) and B = 8.
+Llama-3-8B Q4_K_M shapes.
 
-A step is one decode token's pass over the linear layers of all 32 layers of a random-init
-Llama-3-8B-shaped model in Q4_K_M: per layer norm+quantize, q/k/v in one launch, quantize,
-o (+residual), norm+quantize, gate+up+SiLU-GLU in one launch, quantize, down (+residual),
-exactly as leat's decode step calls them (leat/model.py:497-558 via leat/ops.py:23-55). Weights
-are 32 distinct layers of seeded synthetic blocks (4.41 GB, far beyond the 256 MB MALL), resident
-in HBM before the timed region; each step is one HIP-graph replay. `value` is weight bytes per
-step / step time, as leat's bench counts weight GB/s (leat/bench.py:71-82). The roofline object is
-for the dominant kernel (gate+up GLU matvec): a step's 32 launches of it back to back in a HIP
-graph, timed with HIP events on their stream; the CPU baseline is the C restatement of leat's
-LEAT_KERNELS=ref product (oracle/leat_ref.c) on the host cores, over a bounded sample.
+Headline (config 2, B = 1): a step is one decode token's pass over the linear layers of all 32
+layers of a random-init Llama-3-8B-shaped model in Q4_K_M: per layer norm+quantize, q/k/v in one
+launch, quantize, o (+residual), norm+quantize, gate+up+SiLU-GLU in one launch, quantize, down
+(+residual), exactly as leat's decode step calls them (leat/model.py:497-558 via
+leat/ops.py:23-55), the attention output standing in with q's product. Weights are 32 distinct
+layers of seeded synthetic blocks (4.41 GB, far beyond the 256 MB MALL), resident in HBM before
+the timed region; each step is one HIP-graph replay. `value` is weight bytes per step / step time,
+as leat's bench counts weight GB/s (leat/bench.py:71-82); `linear_tok_s` is that step's rate (the
+linear layers only). The same step runs at B = 4, 8 and 16 ("b4", "b8", "b16"). The roofline
+object is for the dominant kernel (gate+up GLU): a step's 32 launches of it back to back in a HIP
+graph, timed with HIP events on their stream.
 
-Beside the headline line's decode figures it reports, as sub-objects, the other benchmark
-configurations: "prefill" (512 tokens through a layer's FFN on matrix cores, TOPS against the
-int8 MFMA peak) and "moe" (a Qwen3-30B-A3B-style mixture at B = 1 and 8, weight GB/s of the
-distinct chosen experts), each with the roofline of its dominant kernel.
+Beside it, as sub-objects: "decode" (config 3: the full single-stream decode step of the model,
+embedding to argmax with attention over the f16 KV cache and the Q6_K output head, at 1 and 4095
+cached positions: true decode tok/s), "prefill" (config 4: 512 tokens through a layer's FFN on
+matrix cores, TOPS against the int8 MFMA peak; and the down product at 8, 16 and 64 tokens, the
+few-token and split schedules), "moe" (config 5: a Qwen3-30B-A3B-style mixture at B = 1 and 8),
+and "cpu_baseline": the C restatement of leat's LEAT_KERNELS=ref product (oracle/leat_ref.c) on
+config 1 (Q8_0 4096 x 4096) and on one config-2 layer, with all the host's threads and with one.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu] [--legs prefill,moe]
-                    [--copy-probe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--seed S] [--no-cpu]
+                    [--legs decode,prefill,moe,batches] [--copy-probe]
 """
 
 from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import os
 import re
@@ -203,33 +208,50 @@ def measure(torch, lib, layers, B, steps, warmup, device):
     weight_bytes = LAYERS * LAYER_BYTES
     gbs = weight_bytes / (ms * 1e-3) / 1e9
     achieved = glu_bytes(B) / (glu_us * 1e-6) / 1e9
+    traffic, note = profiled_traffic(GLU_KERNELS.get(B, ""))
     return {
         "ms_per_step": ms,
         "weight_gbs": gbs,
         "hbm_frac": gbs / HBM_PEAK_GBS,
-        "tok_s": B * 1000.0 / ms,
+        "linear_tok_s": B * 1000.0 / ms,
         "glu_us": glu_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": profiled_traffic(GLU_KERNELS.get(B, "")),
-                     "traffic_source": "profiles/decode_linear_hbm_bytes.md (rocprofv3 FETCH_SIZE, WRITE_SIZE)",
-                     "kernel": f"gate+up GLU matvec, Q4_K 2x14336x4096, B={B}"
-                               + (" (quantizes its f32 input and its output)" if B <= 2 else ""),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": note,
+                     "kernel": f"gate+up GLU {'matvec' if B <= 8 else 'matrix-core 16-token tiles'}, Q4_K 2x14336x4096, "
+                               f"B={B}" + (" (quantizes its f32 input and its output)" if B <= 2 else ""),
                      "bytes_per_launch": glu_bytes(B)},  # fmt: skip
     }
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_linear_hbm_bytes.md")
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_linear_hbm_bytes.md"
+# the sources of the decode kernels whose HBM bytes that profile records
+TRAFFIC_SOURCES = ["blocks.h", "common.h", "q8.h", "rows.h", "rows.hip", "rowtask.h", "tiles.h", "tiles.hip",
+                   "mmv.h", "mmv.hip", "matvec.hip"]  # fmt: skip
 
 
-def profiled_traffic(kernel: str):
+def sources_sha() -> str:
+    """A digest of the decode kernels' sources, which the traffic profile records beside its bytes."""
+    digest = hashlib.sha256()
+    for name in TRAFFIC_SOURCES:
+        digest.update((ROOT / "leat_amd" / "csrc" / name).read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def profiled_traffic(kernel: str) -> tuple[int | None, str]:
     """HBM bytes per dispatch of `kernel` as the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    records them (calibrated against a copy of known size), or None if it does not."""
+    records them (calibrated against a copy of known size), and where that figure comes from; None
+    where the summary has no line for it, or was measured on other kernel sources than these."""
     try:
-        text = open(TRAFFIC_PROFILE).read()
+        text = TRAFFIC_PROFILE.read_text()
     except OSError:
-        return None
+        return None, "no traffic profile"
+    m = re.search(r"^sources sha ([0-9a-f]+)$", text, re.M)
+    if not m or m.group(1) != sources_sha():
+        return None, f"{TRAFFIC_PROFILE.name} was measured on other kernel sources (sha {m.group(1) if m else '?'})"
     m = re.search(r"^" + re.escape(kernel) + r" (\d+)$", text, re.M)
-    return int(m.group(1)) if m else None
+    if not m:
+        return None, f"{TRAFFIC_PROFILE.name} has no line for this kernel"
+    return int(m.group(1)), f"profiles/{TRAFFIC_PROFILE.name}: rocprofv3 FETCH_SIZE + WRITE_SIZE, sources sha {sources_sha()}"
 
 
 def _graph_us(torch, fn, reps, inner=1):
@@ -251,7 +273,113 @@ def _graph_us(torch, fn, reps, inner=1):
 
 
 # the GLU kernels of the decode legs, as rocprofv3 names them
-GLU_KERNELS = {1: "rows_kernel<12, 1, 2, 4, 8, 2, true, true>", 8: "tiles_kernel<12, 2, 4>"}
+GLU_KERNELS = {1: "rows_kernel<12, 1, 2, 4, 8, 2, true, true>", 4: "tiles_kernel<12, 2, 4>", 8: "tiles_kernel<12, 2, 4>"}
+
+def decode_model(torch, layers, seed, device):
+    """Config 3's model around the config-2 layers' weights (shared, not copied): a Q4_K token
+    embedding (128256 x 4096), the 32 layers, the final norm and a Q6_K output head (128256 x
+    4096), norm weights uniform in [0.5, 1.5), an f16 KV cache of 4096 positions."""
+    from leat_amd.model import LLAMA3_8B, Layer, Model, Weights, _synthetic_blocks
+    from leat_amd.quant import GGMLType, QTensor
+
+    c = LLAMA3_8B
+    gen = torch.Generator(device=device).manual_seed(seed + 7)
+
+    def norm():
+        return torch.rand(c.dim, generator=gen, device=device) + 0.5
+
+    def q(w, name):
+        t, r, cols = next((t, r, cc) for n, t, r, cc in MATRICES if n == name)
+        return QTensor(w[name], GGMLType(t), (r, cols))
+
+    built = [Layer(norm(), q(w, "q"), q(w, "k"), q(w, "v"), q(w, "o"), norm(), q(w, "gate"), q(w, "up"), q(w, "down"))
+             for w in layers]  # fmt: skip
+    weights = Weights(_synthetic_blocks(GGMLType.Q4_K, c.vocab, c.dim, gen, device), built, norm(),
+                      _synthetic_blocks(GGMLType.Q6_K, c.vocab, c.dim, gen, device))  # fmt: skip
+    model = Model(c, weights)
+    for cache in model.cache:  # cached keys and values of a prompt: N(0, 1) in f16
+        cache.normal_(generator=gen)
+    return model
+
+
+def measure_decode(torch, model, steps, device):
+    """Config 3: the full single-stream decode step (embedding, 32 layers with RoPE + KV store and
+    FlashDecoding over the cache, final norm + Q6_K head, argmax) as one HIP-graph replay, at 1
+    and at 4095 cached positions (the step's token at position 0, then at 4095 of a 4096-position
+    cache). tok/s is one token per step; GB/s counts the matrices streamed (layers and head, as
+    leat's bench does) and, for hbm_frac, the keys and values read too."""
+    from leat_amd.model import GraphStep, weight_bytes
+
+    c = model.config
+    step = GraphStep(model, 1, advance=False)  # each replay decodes at the positions the buffer holds
+    w_bytes = weight_bytes(model.weights)
+    out = {"workload": "llama3.1-8b q4_k_m random-init decode step, B=1 (embedding .. argmax)",
+           "weight_bytes_per_token": w_bytes}  # fmt: skip
+    for pos in (0, c.context - 1):
+        step.positions.fill_(pos)
+        step.tokens.fill_(128000)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            step.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            step.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        kv = (pos + 1) * c.layers * 2 * c.kv_heads * c.head_dim * 2
+        out[f"p{pos + 1}"] = {"positions": pos + 1, "ms_per_token": round(ms, 4), "tok_s": round(1000.0 / ms, 1),
+                              "weight_gbs": round(w_bytes / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
+                              "hbm_frac": round((w_bytes + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
+    # the largest single product of a step: the Q6_K head with its fused norm + quantize
+    from leat_amd import kernels
+
+    x = torch.randn(1, 1, c.dim, device=device)
+    norm = (model.weights.output_norm, c.norm_eps)
+    head_us = _graph_us(torch, lambda: kernels.matvecs(x, model.weights.output, norm=norm), steps)
+    head_bytes = model.weights.output.nbytes + c.dim * 4 + c.vocab * 4
+    out["head"] = {"kernel": "Q6_K output head 128256x4096 matvec (RMSNorm + quantize inside)", "us": round(head_us, 2),
+                   "gbs": round(head_bytes / (head_us * 1e-6) / 1e9, 1),
+                   "frac": round(head_bytes / (head_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
+    return out
+
+
+def measure_few_tokens(torch, lib, w, reps, device):
+    """The down product (Q6_K 4096 x 14336, + residual) at 8 tokens (the decode kernels), 16 (the
+    16-token matrix-core tiles, leat's FEW_TOKENS) and 64 (prefill tiles, each tile's K steps split
+    over workgroups): the few-token and split schedules of leat/kernels/matmul.py:904-964."""
+    f32 = dict(dtype=torch.float32, device=device)
+    i32 = dict(dtype=torch.int32, device=device)
+    gen = torch.Generator(device=device).manual_seed(9)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    out = {}
+    for T in (8, 16, 64):
+        h = torch.randn(T, FFN, generator=gen, **f32)
+        q, d, sc = torch.empty(T * FFN // 4, **i32), torch.empty(T * FFN // 32, **f32), torch.empty(T * FFN // 32, **f32)
+        _call(lib, "leat_quantize_q8", h.data_ptr(), T, FFN, None, 0.0, q.data_ptr(), d.data_ptr(), sc.data_ptr(), st())
+        res, y = torch.randn(T, HIDDEN, generator=gen, **f32), torch.empty(T, HIDDEN, **f32)
+        size = int(lib.leat_matmul_workspace(Q6_K, HIDDEN, FFN, T, 0))
+        ws = torch.empty(max(size, 1), dtype=torch.uint8, device=device)
+
+        def run(T=T, q=q, d=d, sc=sc, res=res, y=y, ws=ws, size=size):
+            if T <= 8:
+                _call(lib, "leat_matvec", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, q.data_ptr(), d.data_ptr(),
+                      sc.data_ptr(), T, res.data_ptr(), y.data_ptr(), st())  # fmt: skip
+            else:
+                _call(lib, "leat_matmul", Q6_K, w["down"].data_ptr(), HIDDEN, FFN, q.data_ptr(), d.data_ptr(),
+                      sc.data_ptr(), T, res.data_ptr(), y.data_ptr(), ws.data_ptr() if size else None, size, st())  # fmt: skip
+
+        run()
+        torch.cuda.synchronize()
+        us = _graph_us(torch, run, reps, inner=8)
+        wb = nbytes(Q6_K, HIDDEN, FFN)
+        out[f"t{T}"] = {"us": round(us, 2), "weight_gbs": round(wb / (us * 1e-6) / 1e9, 1),
+                        "tops": round(2 * T * HIDDEN * FFN / (us * 1e-6) / 1e12, 2), "workspace_bytes": size}  # fmt: skip
+    out["t16_over_t8"] = round(out["t16"]["us"] / out["t8"]["us"], 3)
+    return out
+
 
 PREFILL_TOKENS = 512
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
@@ -389,10 +517,12 @@ def moe_layers(torch, device, seed):
             for _ in range(MOE_LAYERS)]  # fmt: skip
 
 
-def cpu_baseline(seconds=10.0, cap=30.0):
-    """leat's LEAT_KERNELS=ref product (f32 activations, dequantize in ggml's order, f32 sums),
-    restated in C with OpenMP, over one synthetic layer's 7 matrices at B=1, repeated for about
-    `seconds` (at most `cap`): weight GB/s, the median layer pass."""
+def cpu_baseline(budget=20.0):
+    """leat's LEAT_KERNELS=ref product (f32 activations, dequantized in ggml's order, f32 sums),
+    restated in C with OpenMP (oracle/leat_ref.c), timed on the host: config 1 (a Q8_0 4096 x 4096
+    matvec, d = f16(|N| * 0.01), int8 quants uniform in [-127, 127], x N(0, 1)) and one config-2
+    layer's 7 matrices at B = 1, each with every thread the process may use and with one; the
+    median pass of each, within about `budget` seconds in all."""
     import numpy as np
 
     from oracle import leat_oracle as O
@@ -405,30 +535,53 @@ def cpu_baseline(seconds=10.0, cap=30.0):
     lib = ctypes.CDLL(str(path))
     lib.leat_ref_linear.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]  # fmt: skip
+    lib.leat_ref_threads.argtypes = [ctypes.c_int]
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     rng = np.random.default_rng(0)
-    mats = [(t, r, c, O.matrix_blocks(t, r, c, rng)) for _, t, r, c in MATRICES]
+    layer = [(t, r, c, O.matrix_blocks(t, r, c, rng)) for _, t, r, c in MATRICES]
+    q8_0 = [(O.Q8_0, 4096, 4096, O.matrix_blocks(O.Q8_0, 4096, 4096, rng))]
     x = {c: rng.standard_normal(c).astype(np.float32) for c in (HIDDEN, FFN)}
     out = np.zeros(FFN, np.float32)
-    times, begin = [], time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        for t, r, c, b in mats:
-            assert lib.leat_ref_linear(t, b.ctypes.data, r, c, x[c].ctypes.data, 1, out.ctypes.data) == 0
-        times.append(time.perf_counter() - t0)
-        elapsed = time.perf_counter() - begin
-        if (elapsed >= seconds and len(times) >= 5) or elapsed >= cap:
-            break
-    per_layer = sorted(times)[len(times) // 2]
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+    def timed(mats, seconds):
+        times, begin = [], time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            for t, r, c, b in mats:
+                assert lib.leat_ref_linear(t, b.ctypes.data, r, c, x[c].ctypes.data, 1, out.ctypes.data) == 0
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - begin >= seconds and len(times) >= 3:
+                break
+        return sorted(times)[len(times) // 2], len(times)
+
+    result = {}
+    for threads in (cores, 1):
+        lib.leat_ref_threads(threads)
+        share = 0.35 if threads > 1 else 0.15
+        c1, n1 = timed(q8_0, budget * share * 0.3)
+        c2, n2 = timed(layer, budget * share * 0.7)
+        result[threads] = {"config1_gbs": round(O.BLOCK[O.Q8_0][1] * 4096 * 4096 / 32 / c1 / 1e9, 2),
+                           "config1_ms": round(c1 * 1e3, 3), "config1_passes": n1,
+                           "layer_gbs": round(LAYER_BYTES / c2 / 1e9, 2), "layer_ms": round(c2 * 1e3, 2),
+                           "layer_passes": n2, "linear_tok_s": round(1.0 / (c2 * LAYERS), 3)}  # fmt: skip
     return {
-        "value": LAYER_BYTES / per_layer / 1e9,
+        "value": result[cores]["layer_gbs"],
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"one Llama-3-8B layer's 7 matrices (q,k,v,o,gate,up Q4_K; down Q6_K; {LAYER_BYTES} B) "
-        f"at B=1, f32 activations, {len(times)} passes in {time.perf_counter() - begin:.1f} s, median",
-        "tok_s_equiv": 1.0 / (per_layer * LAYERS),
+        "sample": f"one config-2 layer's 7 matrices (q,k,v,o,gate,up Q4_K; down Q6_K; {LAYER_BYTES} B) at B=1, "
+        "f32 activations, median pass; and config 1, Q8_0 4096x4096 at B=1",
+        "all_cores": result[cores],
+        "one_core": result[1],
     }
+
+
+def _leg(r):
+    # a config-2 batch size's figures for the JSON line
+    return {"weight_gbs": round(r["weight_gbs"], 1), "hbm_frac": round(r["hbm_frac"], 4),
+            "linear_tok_s": round(r["linear_tok_s"], 1), "ms_per_step": round(r["ms_per_step"], 4),
+            "roofline": r["roofline"]}  # fmt: skip
 
 
 def main():
@@ -438,7 +591,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="prefill,moe", help="configurations beside decode: prefill, moe")
+    ap.add_argument("--legs", default="batches,decode,prefill,moe",
+                    help="configurations beside the headline: batches (B=4, 8, 16), decode, prefill, moe")  # fmt: skip
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 256 MiB device to device: the calibration kernel of HBM byte counters")  # fmt: skip
     args = ap.parse_args()
@@ -462,11 +616,22 @@ def main():
     print(f"weights ready: {LAYERS} layers, {LAYERS * LAYER_BYTES / 1e9:.2f} GB", file=sys.stderr, flush=True)
     b1 = measure(torch, lib, layers, 1, args.steps, args.warmup, device)
     print(f"B=1: {b1['ms_per_step']:.3f} ms/step, {b1['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-    b8 = measure(torch, lib, layers, 8, args.steps, args.warmup, device)
-    print(f"B=8: {b8['ms_per_step']:.3f} ms/step, {b8['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-    prefill = moe = None
+    batches = {}
+    if "batches" in args.legs:
+        for B in (4, 8, 16):
+            batches[f"b{B}"] = _leg(measure(torch, lib, layers, B, args.steps, args.warmup, device))
+            print(f"B={B}: {batches[f'b{B}']['ms_per_step']:.3f} ms/step, {batches[f'b{B}']['weight_gbs']:.0f} GB/s",
+                  file=sys.stderr, flush=True)  # fmt: skip
+    decode = prefill = moe = None
+    if "decode" in args.legs:
+        model = decode_model(torch, layers, args.seed, device)
+        decode = measure_decode(torch, model, max(10, args.steps // 2), device)
+        print(f"decode: P=1 {decode['p1']['tok_s']:.0f} tok/s, P=4096 {decode['p4096']['tok_s']:.0f} tok/s",
+              file=sys.stderr, flush=True)  # fmt: skip
+        del model
     if "prefill" in args.legs:
         prefill = measure_prefill(torch, lib, layers[0], max(5, args.steps // 5), device)
+        prefill["down_by_tokens"] = measure_few_tokens(torch, lib, layers[0], max(5, args.steps // 5), device)
         print(f"prefill: FFN {prefill['ffn_us']:.0f} us, {prefill['tops']:.0f} TOPS", file=sys.stderr, flush=True)
     del layers
     torch.cuda.empty_cache()
@@ -501,11 +666,10 @@ def main():
                    "batch": 1, "layers": LAYERS, "weight_bytes_per_step": LAYERS * LAYER_BYTES,
                    "seed": args.seed},  # fmt: skip
         "hbm_frac": round(b1["hbm_frac"], 4),
-        "tok_s": round(b1["tok_s"], 1),
-        "b8": {"weight_gbs": round(b8["weight_gbs"], 1), "hbm_frac": round(b8["hbm_frac"], 4),
-               "tok_s": round(b8["tok_s"], 1), "ms_per_step": round(b8["ms_per_step"], 4),
-               "roofline": b8["roofline"]},  # fmt: skip
+        "linear_tok_s": round(b1["linear_tok_s"], 1),
+        **batches,
         "roofline": b1["roofline"],
+        "decode": decode,
         "prefill": prefill,
         "moe": moe,
         "cpu_baseline": cpu,

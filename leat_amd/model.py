@@ -139,6 +139,47 @@ def synthetic(config: LlamaConfig, seed: int = 0, device="cuda") -> Weights:
     return Weights(embed, layers, norm(), _synthetic_blocks(q6, c.vocab, c.dim, gen, device))
 
 
+def from_gguf(path, context: int = 4096, slots: int = 1, device="cuda") -> Model:
+    """A Llama-architecture model from a GGUF file (leat/gguf.py's reader, leat/model.py's
+    names for arch "llama"): the sizes from its llama.* metadata, the matrices from its tensors in
+    one transfer, Llama 3.1's RoPE factors from rope_freqs.weight where the file has them."""
+    from leat_amd.gguf import GGUF
+
+    g = GGUF.open(path)
+    m = g.metadata
+    arch = m.get("general.architecture", "llama")
+    if arch != "llama":
+        raise ValueError(f"{path}: architecture {arch!r}; this decoder runs llama")
+    dim, heads = int(m["llama.embedding_length"]), int(m["llama.attention.head_count"])
+    layers = int(m["llama.block_count"])
+    names = ["token_embd.weight", "output_norm.weight", "output.weight"]
+    for i in range(layers):
+        names += [f"blk.{i}.{n}.weight" for n in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm",
+                                                     "ffn_gate", "ffn_up", "ffn_down")]  # fmt: skip
+    if "rope_freqs.weight" in g.tensors:
+        names.append("rope_freqs.weight")
+    t = g.load(device, names)
+    vocab = t["token_embd.weight"].shape[0]
+    config = LlamaConfig(
+        dim=dim, layers=layers, heads=heads, kv_heads=int(m.get("llama.attention.head_count_kv", heads)),
+        head_dim=dim // heads, ffn=int(m["llama.feed_forward_length"]), vocab=vocab,
+        norm_eps=float(m.get("llama.attention.layer_norm_rms_epsilon", 1e-5)),
+        rope_theta=float(m.get("llama.rope.freq_base", 10000.0)), rope_scaling=None, context=context, slots=slots,
+    )  # fmt: skip
+
+    def norm(name: str) -> torch.Tensor:
+        return t[name].dequant()
+
+    built = [Layer(norm(f"blk.{i}.attn_norm.weight"), t[f"blk.{i}.attn_q.weight"], t[f"blk.{i}.attn_k.weight"],
+                   t[f"blk.{i}.attn_v.weight"], t[f"blk.{i}.attn_output.weight"], norm(f"blk.{i}.ffn_norm.weight"),
+                   t[f"blk.{i}.ffn_gate.weight"], t[f"blk.{i}.ffn_up.weight"], t[f"blk.{i}.ffn_down.weight"])
+             for i in range(layers)]  # fmt: skip
+    weights = Weights(t["token_embd.weight"], built, norm("output_norm.weight"), t["output.weight"])
+    factors = t["rope_freqs.weight"].dequant().cpu().tolist() if "rope_freqs.weight" in t else None
+    device_of = t["output.weight"].data.device
+    return Model(config, weights, rope=rope_table(config.head_dim, config.rope_theta, context, factors, device_of))
+
+
 def weight_bytes(w: Weights) -> int:
     """The bytes of matrices a decode step streams: every layer's, and the output head."""
     per_layer = sum(m.nbytes for layer in w.layers for m in (layer.q, layer.k, layer.v, layer.o, layer.gate, layer.up, layer.down))
@@ -166,11 +207,13 @@ class Model:
             self.rope = rope_table(c.head_dim, c.rope_theta, c.context, factors, device)
 
     def logits(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
-               lengths: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
-        """One decode step of `tokens` (B,) int32, row b the token of the sequence in cache slot
-        slots[b] at position positions[b] (device tensors): the logits (B, vocab) f32. Row b's
-        keys and values go to its slot at its position, and it attends over positions
-        0..positions[b] (lengths, positions + 1, may be given to save the addition)."""
+               lengths: torch.Tensor | None = None, last: bool = False) -> torch.Tensor:  # fmt: skip
+        """One step of `tokens` (B,) int32, row b the token of the sequence in cache slot slots[b]
+        at position positions[b] (device tensors): the logits (B, vocab) f32. Row b's keys and
+        values go to its slot at its position, and it attends over positions 0..positions[b]
+        (lengths, positions + 1, may be given to save the addition). Rows of one sequence's
+        consecutive positions are a chunk of its prompt, each row seeing those before it; with
+        `last`, only the last row's logits are computed, (1, vocab)."""
         c, w = self.config, self.weights
         B = tokens.shape[0]
         if lengths is None:
@@ -185,18 +228,22 @@ class Model:
             att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context)
             x = ops.linear(att, layer.o, residual=x)
             x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))
+        if last:
+            x, B = x[:, -1:], 1
         (logits,) = ops.linears(x, w.output, norm=(w.output_norm, c.norm_eps))
         return logits.view(B, c.vocab)
 
     def step(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
-             lengths: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
-        """The greedy next token of each row: argmax of logits(), (B,) int32."""
-        return ops.argmax(self.logits(tokens, slots, positions, lengths)).view(-1)
+             lengths: torch.Tensor | None = None, last: bool = False) -> torch.Tensor:  # fmt: skip
+        """The greedy next token of each row (of the last only, with `last`): argmax of logits(),
+        (B,) int32."""
+        return ops.argmax(self.logits(tokens, slots, positions, lengths, last)).view(-1)
 
 
 class GraphStep:
     """A decode step of B rows captured once as a HIP graph over static device buffers `tokens`,
-    `slots` and `positions` (B,) int32; replay() runs it on whatever the buffers hold and leaves
+    `slots` and `positions` (B,) int32, which the caller fills before replaying (building the
+    graph writes nothing to the cache); replay() runs it on whatever the buffers hold and leaves
     the next tokens in `next`. With `advance`, the graph also moves each row on: tokens = next,
     positions += 1, so replays decode one token after another with no host work between them."""
 
@@ -204,8 +251,9 @@ class GraphStep:
         device = model.weights.output.data.device
         self.model, self.batch = model, batch
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=device)
-        self.slots = torch.arange(batch, dtype=torch.int32, device=device)
-        self.positions = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.slots = torch.zeros(batch, dtype=torch.int32, device=device)
+        # past the cache's positions: the eager warm-up below stores no key or value anywhere
+        self.positions = torch.full((batch,), model.config.context, dtype=torch.int32, device=device)
         self.lengths = torch.ones(batch, dtype=torch.int32, device=device)
         self._run(advance=False)  # once eagerly: every launch checked, and the memory pool warmed
         torch.cuda.synchronize(device)

@@ -140,3 +140,8 @@ int leat_ref_linear(int type, const uint8_t *w, int64_t rows, int64_t cols, cons
     }
     return 0;
 }
+
+/* The OpenMP threads the functions above use (the CPU baseline times all cores, then one). */
+#include <omp.h>
+void leat_ref_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int leat_ref_max_threads(void) { return omp_get_max_threads(); }

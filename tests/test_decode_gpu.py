@@ -173,6 +173,7 @@ def test_graph_step_replays_eager(cuda):
     graphed, eager = Model(cfg, weights), Model(cfg, weights)
     step = GraphStep(graphed, 2)
     step.tokens.copy_(torch.tensor([5, 9], dtype=torch.int32))
+    step.slots.copy_(torch.arange(2, dtype=torch.int32))
     step.positions.zero_()
     tokens = torch.tensor([5, 9], dtype=torch.int32, device=cuda)
     slots = torch.arange(2, dtype=torch.int32, device=cuda)
