@@ -37,6 +37,8 @@ struct Dots {
 template <>
 struct Task<Q4_K> {
     static constexpr int BYTES = 144, WEIGHTS = 256, TASK_W = 32, PER_BLOCK = 8, WORDS = 4;
+    static constexpr bool NEEDS_S = true;  // the mins enter through s = d * sum(q)
+    static constexpr int WORD_SKIP = 0;    // span 1's words start where span 0's do, in its own group
     struct Raw {
         u32x4 hdr, qs;
     };
@@ -103,6 +105,8 @@ struct Task<Q4_K> {
 template <>
 struct Task<Q6_K> {
     static constexpr int BYTES = 210, WEIGHTS = 256, TASK_W = 32, PER_BLOCK = 8, WORDS = 4;
+    static constexpr bool NEEDS_S = false;
+    static constexpr int WORD_SKIP = 0;
     struct Raw {
         uint32_t ql[4], qh[4];
         uint32_t sc;  // the two int8 scales, in bytes 0 and 1
@@ -166,6 +170,8 @@ struct Task<Q6_K> {
 template <>
 struct Task<Q8_0> {
     static constexpr int BYTES = 34, WEIGHTS = 32, TASK_W = 64, PER_BLOCK = 1, WORDS = 8;
+    static constexpr bool NEEDS_S = false;
+    static constexpr int WORD_SKIP = 0;
     struct Raw {
         uint32_t v[17];
     };
@@ -218,6 +224,12 @@ struct Task<Q8_0> {
     }
 };
 
+}  // namespace leat
+
+#include "tasks.h"
+
+namespace leat {
+
 // token t's activations for a task: xq (tokens * cols/4 words), xd/xs (tokens * cols/32)
 template <int TYPE, bool SCALES = true>
 __device__ __forceinline__ ActQ load_act(const int32_t* xq, const float* xd, const float* xs, int cols,
@@ -231,7 +243,7 @@ __device__ __forceinline__ ActQ load_act(const int32_t* xq, const float* xd, con
 #pragma unroll
     for (int i = 0; i < T::WORDS; i += 4) {
         u32x4 v0 = *(const u32x4*)(q + g0 * 8 + word + i);
-        u32x4 v1 = *(const u32x4*)(q + g1 * 8 + word + i);
+        u32x4 v1 = *(const u32x4*)(q + g1 * 8 + word + T::WORD_SKIP + i);
         a.x0[i] = v0[0], a.x0[i + 1] = v0[1], a.x0[i + 2] = v0[2], a.x0[i + 3] = v0[3];
         a.x1[i] = v1[0], a.x1[i + 1] = v1[1], a.x1[i + 2] = v1[2], a.x1[i + 3] = v1[3];
     }
@@ -239,7 +251,7 @@ __device__ __forceinline__ ActQ load_act(const int32_t* xq, const float* xd, con
     if (!SCALES) return a;
     a.d0 = dd[g0];
     a.d1 = dd[g1];
-    if (TYPE == Q4_K) {
+    if (T::NEEDS_S) {
         const float* ss = xs + (int64_t)t * (cols / GROUP);
         a.s0 = ss[g0];
         a.s1 = ss[g1];
@@ -261,14 +273,14 @@ __device__ __forceinline__ ActQ load_act_lds(const uint32_t* lds, int tokens, in
 #pragma unroll
     for (int i = 0; i < T::WORDS; i += 4) {
         u32x4 v0 = *(const u32x4*)(q + g0 * 8 + word + i);
-        u32x4 v1 = *(const u32x4*)(q + g1 * 8 + word + i);
+        u32x4 v1 = *(const u32x4*)(q + g1 * 8 + word + T::WORD_SKIP + i);
         a.x0[i] = v0[0], a.x0[i + 1] = v0[1], a.x0[i + 2] = v0[2], a.x0[i + 3] = v0[3];
         a.x1[i] = v1[0], a.x1[i + 1] = v1[1], a.x1[i + 2] = v1[2], a.x1[i + 3] = v1[3];
     }
     a.d0 = dd[g0];
     a.d1 = dd[g1];
     a.s0 = a.s1 = 0.0f;
-    if (TYPE == Q4_K) {
+    if (T::NEEDS_S) {
         a.s0 = ss[g0];
         a.s1 = ss[g1];
     }

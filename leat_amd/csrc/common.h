@@ -13,7 +13,10 @@
 
 namespace leat {
 
-enum GgmlType : int { Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+enum GgmlType : int {
+    Q4_0 = 2, Q4_1 = 3, Q5_0 = 6, Q5_1 = 7, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14,
+    IQ4_NL = 20, IQ4_XS = 23, MXFP4 = 39
+};
 
 constexpr int WAVE = 64;
 constexpr int GROUP = 32;

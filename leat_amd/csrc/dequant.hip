@@ -3,69 +3,20 @@
 // own, no fused multiply-add), the LEAT_KERNELS=ref linear layer on it (leat/ops.py:35-38: f32
 // activations, not quantized), and the exact int32 span sums of the int8 path for parity tests.
 #include "blocks.h"
+#include "formats.h"
 
 namespace leat {
-
-// the 32 weights of piece p of a row: Q4_K sub-block p, Q6_K row-of-32 p (half p/4, k = p%4),
-// Q8_0 block p
-template <int TYPE>
-__device__ void dequant_piece(const uint8_t* __restrict__ blk, int p, float y[32]) {
-#pragma clang fp contract(off)
-    if (TYPE == Q8_0) {
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8)));
-#pragma unroll
-        for (int l = 0; l < 32; l++) y[l] = d * (float)(int8_t)blk[2 + l];
-    } else if (TYPE == Q4_K) {
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[0] | (blk[1] << 8)));
-        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[2] | (blk[3] << 8)));
-        const uint8_t* q = blk + 4;
-        int sc, m;
-        if (p < 4) {
-            sc = q[p] & 63;
-            m = q[p + 4] & 63;
-        } else {
-            sc = (q[p + 4] & 0xF) | ((q[p - 4] >> 6) << 4);
-            m = (q[p + 4] >> 4) | ((q[p] >> 6) << 4);
-        }
-        const float d1 = d * (float)sc, m1 = dmin * (float)m;
-        const uint8_t* qs = blk + 16 + 32 * (p >> 1);
-        const int shift = 4 * (p & 1);
-#pragma unroll
-        for (int l = 0; l < 32; l++) y[l] = d1 * (float)((qs[l] >> shift) & 0xF) - m1;
-    } else {
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(blk[208] | (blk[209] << 8)));
-        const int n = p >> 2, k = p & 3;
-        const uint8_t* ql = blk + 64 * n + 32 * (k & 1);
-        const uint8_t* qh = blk + 128 + 32 * n;
-        const int8_t* sc = (const int8_t*)(blk + 192 + 8 * n + 2 * k);
-        const int lshift = 4 * (k >> 1), hshift = 2 * k;
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const int q = (((ql[l] >> lshift) & 0xF) | (((qh[l] >> hshift) & 3) << 4)) - 32;
-            y[l] = d * (float)sc[l >> 4] * (float)q;
-        }
-    }
-}
-
-template <int TYPE>
-constexpr int block_bytes() {
-    return TYPE == Q8_0 ? 34 : TYPE == Q4_K ? 144 : 210;
-}
-template <int TYPE>
-constexpr int block_weights() {
-    return TYPE == Q8_0 ? 32 : 256;
-}
 
 template <int TYPE>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ blocks, int64_t pieces,
                                                       float* __restrict__ out) {
-    constexpr int PER = block_weights<TYPE>() / 32;
+    constexpr int PER = Format<TYPE>::WEIGHTS / 32;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= pieces) return;
     const int64_t b = i / PER;
     const int p = (int)(i % PER);
     float y[32];
-    dequant_piece<TYPE>(blocks + b * block_bytes<TYPE>(), p, y);
+    dequant_piece<TYPE>(blocks + b * Format<TYPE>::BYTES, p, y);
     float* o = out + i * 32;
 #pragma unroll
     for (int l = 0; l < 32; l += 4) *(float4*)(o + l) = make_float4(y[l], y[l + 1], y[l + 2], y[l + 3]);
@@ -75,15 +26,15 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 template <int TYPE>
 __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t* __restrict__ w, int rows, int cols,
                                                         const int32_t* __restrict__ ids, float* __restrict__ out) {
-    constexpr int PER = block_weights<TYPE>() / 32;
+    constexpr int PER = Format<TYPE>::WEIGHTS / 32;
     const int t = blockIdx.y, pieces = cols / 32;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= pieces) return;
     const int id = ids[t];
     float y[32];
     if (id >= 0 && id < rows) {
-        const int64_t nb = cols / block_weights<TYPE>();
-        dequant_piece<TYPE>(w + ((int64_t)id * nb + p / PER) * block_bytes<TYPE>(), p % PER, y);
+        const int64_t nb = cols / Format<TYPE>::WEIGHTS;
+        dequant_piece<TYPE>(w + ((int64_t)id * nb + p / PER) * Format<TYPE>::BYTES, p % PER, y);
     } else {
 #pragma unroll
         for (int l = 0; l < 32; l++) y[l] = 0.0f;
@@ -100,17 +51,17 @@ __global__ __launch_bounds__(256) void matvec_f32x_kernel(const uint8_t* __restr
                                                           const float* __restrict__ x,
                                                           const float* __restrict__ residual,
                                                           float* __restrict__ out) {
-    constexpr int PER = block_weights<TYPE>() / 32;
+    constexpr int PER = Format<TYPE>::WEIGHTS / 32;
     const int lane = threadIdx.x & (WAVE - 1);
     const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / WAVE);
     if (row >= rows) return;
-    const int nb = cols / block_weights<TYPE>(), pieces = cols / 32;
+    const int nb = cols / Format<TYPE>::WEIGHTS, pieces = cols / 32;
     float acc[B];
 #pragma unroll
     for (int t = 0; t < B; t++) acc[t] = 0.0f;
     for (int p = lane; p < pieces; p += WAVE) {
         float y[32];
-        dequant_piece<TYPE>(w + ((int64_t)row * nb + p / PER) * block_bytes<TYPE>(), p % PER, y);
+        dequant_piece<TYPE>(w + ((int64_t)row * nb + p / PER) * Format<TYPE>::BYTES, p % PER, y);
 #pragma unroll
         for (int t = 0; t < B; t++) {
             const float* xt = x + (int64_t)t * cols + (int64_t)p * 32;
@@ -154,11 +105,13 @@ __global__ __launch_bounds__(256) void group_dots_kernel(const uint8_t* __restri
         int32_t* o = out + ((int64_t)t * rows + row) * spans;
         o[2 * g0 + word / 4] = dd.a;
         o[2 * g1 + word / 4] = dd.b;
-    } else if (TYPE == Q4_K) {  // two tasks (halves h) add up to a group: the h = 1 lane adds
+    } else if (TYPE == Q4_K || TYPE == Q5_K) {  // two tasks (halves h) add up to a group: the h = 1 lane adds
         const int spans = cols / 32;
         int32_t* o = out + ((int64_t)t * rows + row) * spans;
         atomicAdd(o + g0, dd.a);
         atomicAdd(o + g1, dd.b);
+    } else if (TYPE == IQ4_XS) {  // a task is one group, its two halves of 16
+        out[((int64_t)t * rows + row) * (cols / 32) + g0] = dd.a + dd.b;
     } else {
         const int spans = cols / 32;
         int32_t* o = out + ((int64_t)t * rows + row) * spans;
@@ -179,25 +132,35 @@ int check_ptrs(int type, const void* w, const void* xq);
 
 using namespace leat;
 
+// a row length of whole blocks of `type` (any type the dequantizer decodes)
+static int check_format_cols(int type, int cols, const char* what) {
+    int weights = 0;
+    switch (type) {
+#define LEAT_WEIGHTS(T) \
+    case T: weights = Format<T>::WEIGHTS; break;
+        LEAT_FORMATS(LEAT_WEIGHTS)
+#undef LEAT_WEIGHTS
+    default: set_error("%s: unsupported type %d", what, type); return -1;
+    }
+    LEAT_REQUIRE(cols > 0 && cols % weights == 0, "%s: cols %d is not a whole number of %d-weight blocks", what, cols,
+                 weights);
+    return 0;
+}
+
 extern "C" int leat_dequantize(int type, const void* blocks, int64_t n_blocks, float* out, void* stream) {
     LEAT_REQUIRE(blocks && out && n_blocks >= 0, "dequantize: null pointer");
     if (n_blocks == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     const uint8_t* b = (const uint8_t*)blocks;
-    int64_t pieces;
     switch (type) {
-    case Q8_0:
-        pieces = n_blocks;
-        hipLaunchKernelGGL(dequant_kernel<Q8_0>, dim3((pieces + 255) / 256), dim3(256), 0, st, b, pieces, out);
-        break;
-    case Q4_K:
-        pieces = n_blocks * 8;
-        hipLaunchKernelGGL(dequant_kernel<Q4_K>, dim3((pieces + 255) / 256), dim3(256), 0, st, b, pieces, out);
-        break;
-    case Q6_K:
-        pieces = n_blocks * 8;
-        hipLaunchKernelGGL(dequant_kernel<Q6_K>, dim3((pieces + 255) / 256), dim3(256), 0, st, b, pieces, out);
-        break;
+#define LEAT_DEQUANT(T)                                                                                        \
+    case T: {                                                                                                  \
+        const int64_t pieces = n_blocks * (Format<T>::WEIGHTS / 32);                                           \
+        hipLaunchKernelGGL(dequant_kernel<T>, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, b, pieces, out); \
+        break;                                                                                                 \
+    }
+        LEAT_FORMATS(LEAT_DEQUANT)
+#undef LEAT_DEQUANT
     default: set_error("dequantize: unsupported type %d", type); return -1;
     }
     return check_launch("dequantize");
@@ -207,15 +170,17 @@ extern "C" int leat_embedding(int type, const void* w, int rows, int cols, const
                               void* stream) {
     LEAT_REQUIRE(w && ids && out && rows > 0, "embedding: null pointer or empty matrix");
     LEAT_REQUIRE(tokens >= 0 && tokens <= 65535, "embedding: %d tokens", tokens);
-    if (check_cols(type, cols)) return -1;
+    if (check_format_cols(type, cols, "embedding")) return -1;
     if (tokens == 0) return 0;
     const dim3 grid((cols / 32 + 255) / 256, tokens);
     hipStream_t st = (hipStream_t)stream;
     const uint8_t* b = (const uint8_t*)w;
     switch (type) {
-    case Q8_0: hipLaunchKernelGGL(embedding_kernel<Q8_0>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
-    case Q4_K: hipLaunchKernelGGL(embedding_kernel<Q4_K>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
-    default: hipLaunchKernelGGL(embedding_kernel<Q6_K>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
+#define LEAT_EMBED(T) \
+    case T: hipLaunchKernelGGL(embedding_kernel<T>, grid, dim3(256), 0, st, b, rows, cols, ids, out); break;
+        LEAT_FORMATS(LEAT_EMBED)
+#undef LEAT_EMBED
+    default: break;
     }
     return check_launch("embedding");
 }
@@ -236,15 +201,17 @@ static int f32x_t(const uint8_t* w, int rows, int cols, const float* x, int toke
 
 extern "C" int leat_matvec_f32x(int type, const void* w, int rows, int cols, const float* x, int tokens,
                                 const float* residual, float* out, void* stream) {
-    if (check_cols(type, cols)) return -1;
+    if (check_format_cols(type, cols, "matvec_f32x")) return -1;
     LEAT_REQUIRE(w && x && out && rows > 0, "matvec_f32x: null pointer or empty matrix");
     LEAT_REQUIRE((uintptr_t)x % 16 == 0, "matvec_f32x: activations must start 16-byte aligned");
     const uint8_t* b = (const uint8_t*)w;
     hipStream_t st = (hipStream_t)stream;
     switch (type) {
-    case Q8_0: return f32x_t<Q8_0>(b, rows, cols, x, tokens, residual, out, st);
-    case Q4_K: return f32x_t<Q4_K>(b, rows, cols, x, tokens, residual, out, st);
-    default: return f32x_t<Q6_K>(b, rows, cols, x, tokens, residual, out, st);
+#define LEAT_F32X(T) \
+    case T: return f32x_t<T>(b, rows, cols, x, tokens, residual, out, st);
+        LEAT_FORMATS(LEAT_F32X)
+#undef LEAT_F32X
+    default: return -1;
     }
 }
 
@@ -255,18 +222,23 @@ extern "C" int leat_group_dots(int type, const void* w, int rows, int cols, cons
     if (check_ptrs(type, w, xq)) return -1;
     hipStream_t st = (hipStream_t)stream;
     const uint8_t* b = (const uint8_t*)w;
-    const int task_w = type == Q8_0 ? 64 : 32;
-    const int64_t n = (int64_t)tokens * rows * (cols / task_w);
-    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
-    switch (type) {
-    case Q8_0: hipLaunchKernelGGL(group_dots_kernel<Q8_0>, grid, block, 0, st, b, rows, cols, xq, tokens, out); break;
-    case Q4_K: {
+    const bool halves = type == Q4_K || type == Q5_K;  // two tasks add into each group: cleared first
+    if (halves) {
         const int64_t spans = (int64_t)tokens * rows * (cols / 32);
         hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((spans + 255) / 256)), dim3(256), 0, st, out, spans);
-        hipLaunchKernelGGL(group_dots_kernel<Q4_K>, grid, block, 0, st, b, rows, cols, xq, tokens, out);
-        break;
     }
-    default: hipLaunchKernelGGL(group_dots_kernel<Q6_K>, grid, block, 0, st, b, rows, cols, xq, tokens, out); break;
+    switch (type) {
+#define LEAT_DOTS(T)                                                                                                \
+    case T: {                                                                                                       \
+        const int64_t n = (int64_t)tokens * rows * (cols / Task<T>::TASK_W);                                        \
+        hipLaunchKernelGGL(group_dots_kernel<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, b, rows, cols, \
+                           xq, tokens, out);                                                                        \
+        break;                                                                                                      \
+    }
+        LEAT_DOTS(Q4_0) LEAT_DOTS(Q4_1) LEAT_DOTS(Q5_0) LEAT_DOTS(Q5_1) LEAT_DOTS(Q8_0) LEAT_DOTS(Q4_K) LEAT_DOTS(Q5_K)
+        LEAT_DOTS(Q6_K) LEAT_DOTS(IQ4_NL) LEAT_DOTS(IQ4_XS) LEAT_DOTS(MXFP4)
+#undef LEAT_DOTS
+    default: set_error("group_dots: unsupported type %d", type); return -1;
     }
     return check_launch("group_dots");
 }

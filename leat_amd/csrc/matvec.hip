@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(MatvecArgs args) {
         float* lds_d = (float*)(act_lds + words);
         for (int i = threadIdx.x; i < scales; i += blockDim.x) {
             lds_d[i] = args.xd[i];
-            if (TYPE == Q4_K) lds_d[scales + i] = args.xs[i];
+            if (T::NEEDS_S) lds_d[scales + i] = args.xs[i];
         }
         __syncthreads();
     }
@@ -185,12 +185,16 @@ static int launch_t(MatvecArgs& a, int tokens, hipStream_t s) {
     }
 }
 
+// X(TYPE) for every type the decode tasks take (blocks.h, tasks.h)
+#define LEAT_TASK_TYPES(X) X(Q4_0) X(Q4_1) X(Q5_0) X(Q5_1) X(Q8_0) X(Q4_K) X(Q5_K) X(Q6_K) X(IQ4_NL) X(IQ4_XS) X(MXFP4)
+
 template <int MODE>
 static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     switch (type) {
-    case Q4_K: return launch_t<Q4_K, MODE>(a, tokens, s);
-    case Q6_K: return launch_t<Q6_K, MODE>(a, tokens, s);
-    case Q8_0: return launch_t<Q8_0, MODE>(a, tokens, s);
+#define LEAT_LAUNCH(T) \
+    case T: return launch_t<T, MODE>(a, tokens, s);
+        LEAT_TASK_TYPES(LEAT_LAUNCH)
+#undef LEAT_LAUNCH
     default: set_error("matvec: unsupported type %d", type); return -1;
     }
 }
@@ -263,17 +267,20 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
 // Q4_K blocks are read as 16-byte vectors: their matrices start 16-byte aligned; Q6_K and Q8_0
 // blocks as aligned dwords from a 4-byte aligned start. Activation words are read 16 at a time.
 int check_ptrs(int type, const void* w, const void* xq) {
-    const uintptr_t need = type == Q4_K ? 16 : 4;
+    // Q4_K and Q5_K blocks are read in 16-byte pieces, IQ4_XS in 8-byte ones, the 32-weight types
+    // other than Q8_0 in halfwords
+    const uintptr_t need = type == Q4_K || type == Q5_K ? 16 : type == IQ4_XS ? 8 : type == Q8_0 || type == Q6_K ? 4 : 2;
     LEAT_REQUIRE((uintptr_t)w % need == 0, "weights of type %d must start %d-byte aligned", type, (int)need);
     LEAT_REQUIRE(xq == nullptr || (uintptr_t)xq % 16 == 0, "activation words must start 16-byte aligned");
     return 0;
 }
 
 int check_cols(int type, int cols) {
-    if (type == Q4_K || type == Q6_K) {
+    if (type == Q4_K || type == Q5_K || type == Q6_K || type == IQ4_XS) {
         LEAT_REQUIRE(cols > 0 && cols % 256 == 0, "cols %d is not a whole number of 256-weight blocks", cols);
-    } else if (type == Q8_0) {
-        LEAT_REQUIRE(cols > 0 && cols % 64 == 0, "cols %d is not a whole number of Q8_0 block pairs", cols);
+    } else if (type == Q8_0 || type == Q4_0 || type == Q4_1 || type == Q5_0 || type == Q5_1 || type == IQ4_NL ||
+               type == MXFP4) {
+        LEAT_REQUIRE(cols > 0 && cols % 64 == 0, "cols %d is not a whole number of block pairs", cols);
     } else {
         set_error("unsupported type %d", type);
         return -1;

@@ -398,8 +398,32 @@ int64_t matmul_workspace(int type, int rows, int cols, int tokens, bool gated) {
     return workspace_of(type, rows, cols, tokens, gated);
 }
 
+// the storage types without matrix-core tiles here (Q4_0, Q4_1, Q5_0, Q5_1, Q5_K, IQ4_NL, IQ4_XS,
+// MXFP4): their products run on the decode kernels' v_dot4 tasks, 8 tokens a launch, so the int8
+// arithmetic is the decode path's and the weights are read once per 8 tokens
+static bool tileless(int type) { return type != Q4_K && type != Q6_K && type != Q8_0; }
+
+static int chunked(int type, const void* const* ws, int rows, int cols, const int32_t* xq, const float* xd,
+                   const float* xs, int tokens, const float* residual, int kind, float* out, hipStream_t st) {
+    for (int t0 = 0; t0 < tokens; t0 += 8) {
+        const int n = std::min(8, tokens - t0);
+        const int32_t* q = xq + (int64_t)t0 * (cols / 4);
+        const float *d = xd + (int64_t)t0 * (cols / GROUP), *s = xs + (int64_t)t0 * (cols / GROUP);
+        float* o = out + (int64_t)t0 * rows;
+        const int status = kind < 0 ? leat_matvec(type, ws[0], rows, cols, q, d, s, n, residual ? residual + (int64_t)t0 * rows : nullptr,
+                                                  o, st)
+                                    : leat_glu_matvec(type, ws[0], ws[1], rows, cols, q, d, s, n, kind, o, st);  // fmt: skip
+        if (status) return -1;
+    }
+    return 0;
+}
+
 int matmul_go(int type, const void* w, int rows, int cols, const int32_t* xq, const float* xd, const float* xs,
               int tokens, const float* residual, float* out, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+    if (tileless(type)) {
+        LEAT_REQUIRE(w && xq && xd && xs && out && rows > 0 && tokens > 0, "matmul: null pointer or empty product");
+        return chunked(type, &w, rows, cols, xq, xd, xs, tokens, residual, -1, out, st);
+    }
     if (mmq_check(type, w, rows, cols, xq, xd, xs, tokens, out)) return -1;
     if (few_fits(type, cols, tokens, &w, 1))
         return few_launch(type, residual ? MMV_RESIDUAL : MMV_PLAIN, &w, 1, rows, cols, xq, xd, xs, tokens, residual, 0,
@@ -436,6 +460,12 @@ extern "C" int leat_matmul(int type, const void* w, int rows, int cols, const in
 extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,
                                const float* xd, const float* xs, int tokens, int kind, float* out, void* workspace,
                                int64_t workspace_bytes, void* stream) {
+    if (tileless(type)) {
+        LEAT_REQUIRE(gate && up && xq && xd && xs && out && rows > 0 && tokens > 0, "glu_matmul: null pointer or empty product");
+        LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul: unknown GLU kind %d", kind);
+        const void* ws[2] = {gate, up};
+        return chunked(type, ws, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream);
+    }
     if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, out) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, out))
         return -1;
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul: unknown GLU kind %d", kind);

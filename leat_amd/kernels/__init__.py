@@ -25,7 +25,7 @@ from leat_amd.kernels.attention import (
     supports_embedding,
     supports_rotate,
 )
-from leat_amd.quant import BLOCK, KERNEL_TYPES, GGMLType, QTensor
+from leat_amd.quant import BLOCK, KERNEL_TYPES, MATVEC_TYPES, GGMLType, QTensor
 
 GROUP = 32  # int8 activations sharing one scale (leat/kernels/common.py:20)
 MATVEC_TOKENS = 8  # the most tokens the decode kernels take (leat/kernels/matvec.py:36)
@@ -130,7 +130,7 @@ def supports_matvec(x: torch.Tensor, w: QTensor) -> bool:
     in a type these kernels decode, on a gfx950 GPU."""
     if not (0 < _rows_of(x) <= MATVEC_TOKENS):
         return False
-    return w.type in KERNEL_TYPES and w.shape[1] % 64 == 0 and _on_gfx950(x)
+    return w.type in MATVEC_TYPES and w.shape[1] % 64 == 0 and _on_gfx950(x)
 
 
 def matvecs(
@@ -250,7 +250,11 @@ def _single_sequence(x: torch.Tensor) -> bool:
 def matmul_fits(ggml_type: GGMLType, rows: int, cols: int) -> bool:
     """Shapes the prefill tiles take (leat/kernels/matmul.py:1041-1044): rows in 64s, rows of
     whole 256-weight steps, and row byte lengths that keep every block 4-byte aligned."""
-    if ggml_type not in KERNEL_TYPES or rows % 64 != 0 or cols % 256 != 0:
+    if ggml_type not in MATVEC_TYPES or rows % 64 != 0:
+        return False
+    if ggml_type not in KERNEL_TYPES:  # the decode tasks, 8 tokens a launch: whole pairs of blocks
+        return cols % 64 == 0 and cols % BLOCK[ggml_type][0] == 0
+    if cols % 256 != 0:
         return False
     elements, size = BLOCK[ggml_type]
     return cols // elements * size % 4 == 0

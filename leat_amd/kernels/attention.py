@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from leat_amd import _lib
-from leat_amd.quant import BLOCK, KERNEL_TYPES, NATIVE, QTensor
+from leat_amd.quant import BLOCK, DEQUANT_TYPES, NATIVE, QTensor
 
 HEAD_DIM = 128  # the head dimension the attention kernel takes
 
@@ -120,7 +120,7 @@ def argmax(x: torch.Tensor) -> torch.Tensor:
 
 def supports_embedding(w: QTensor) -> bool:
     """A matrix in a type these kernels decode (rows whole numbers of blocks)."""
-    return w.type in KERNEL_TYPES and w.shape[1] % BLOCK[w.type][0] == 0 and _on_gfx950(w.data)
+    return w.type in DEQUANT_TYPES and w.shape[1] % BLOCK[w.type][0] == 0 and _on_gfx950(w.data)
 
 
 def embedding(tokens: torch.Tensor, w: QTensor) -> torch.Tensor:
