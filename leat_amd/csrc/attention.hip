@@ -69,11 +69,11 @@ __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
 
 // --------------------------------------------------------------------------------- attention
 
-constexpr int ATT_WAVES = 2;                 // waves a workgroup: 64 keys each
-constexpr int ATT_KEYS = ATT_WAVES * WAVE;   // keys a workgroup takes per round
-constexpr int ATT_CHUNKS = 64;               // most workgroups per (row, kv head): longer rows loop
-constexpr int ATT_GROUP = 8;                 // most query heads sharing a kv head
-constexpr int ATT_DIM = 128;                 // head dimension
+constexpr int ATT_WAVES = 4;                       // waves a workgroup
+constexpr int ATT_WAVE_KEYS = 32;                  // keys a wave takes per round
+constexpr int ATT_KEYS = ATT_WAVES * ATT_WAVE_KEYS;  // keys a workgroup takes per round
+constexpr int ATT_CHUNKS = 64;                     // most workgroups per (row, kv head): longer rows loop
+constexpr int ATT_DIM = 128;                       // head dimension: a pair of dimensions a lane
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG = -1e30f;  // a finite floor: a fully masked wave never computes -inf - -inf
 
@@ -86,19 +86,47 @@ struct AttentionArgs {
     const int32_t* lengths;   // rows: keys 0 .. length - 1 of the row's slot
     int chunks;               // workgroups per (row, kv head)
     float scale;
-    float* partial;  // (rows * heads, chunks, dim + 2): unnormalized output, then max and sum
+    float* partial;  // (rows * heads, chunks, dim + 2): unnormalized output, then max (log2 units) and sum
     float* out;      // (rows, heads * dim)
 };
 
-// A workgroup per (row, kv head, chunk): the group's query heads over keys chunk * ATT_KEYS + 64w +
-// lane, then every chunks-th round after. Lane = key while scoring (the key's 128 values from
-// 16-byte loads), lane = a pair of dimensions while the weighted values are summed (a key's
-// values one coalesced 256-byte read), an online softmax across rounds; the waves' sums merge
+// 16 values of each lane summed over the wave's 64 lanes, transposed: lane l ends with the sum of
+// value ((l >> 2) & 15). Each step keeps half the values and adds the partner lane's other half,
+// so 16 sums over 64 lanes take 8 + 4 + 2 + 1 exchanges and 2 more within each quad of lanes.
+// The step sizes are template arguments so that every register index is a constant: a run-time
+// index into v would compile to a compare-and-select chain over the whole array.
+template <int HALF, int MASK>
+__device__ __forceinline__ void transpose_step(float (&v)[16], int lane) {
+    const bool upper = lane & MASK;
+#pragma unroll
+    for (int i = 0; i < HALF; i++) {
+        const float keep = upper ? v[HALF + i] : v[i], give = upper ? v[i] : v[HALF + i];
+        v[i] = keep + __shfl_xor(give, MASK, WAVE);
+    }
+}
+
+__device__ __forceinline__ float transpose_sum16(float (&v)[16], int lane) {
+    transpose_step<8, 32>(v, lane);
+    transpose_step<4, 16>(v, lane);
+    transpose_step<2, 8>(v, lane);
+    transpose_step<1, 4>(v, lane);
+    float s = v[0];
+    s += __shfl_xor(s, 1, WAVE);
+    s += __shfl_xor(s, 2, WAVE);
+    return s;
+}
+
+// A workgroup per (row, kv head, chunk): its waves take ATT_WAVE_KEYS keys each a round, from key
+// chunk * ATT_KEYS + 32 w, then every chunks * ATT_KEYS keys on. Lane l holds dimensions 2l, 2l + 1
+// of the group's queries (scaled by scale * log2 e, so scores are in log2 units) and reads the
+// same two of each key: every key is one coalesced 256-byte read. The keys' 32 partial dot
+// products of each lane are summed across the wave by transpose_sum16, the scores go through LDS
+// to lanes a key each for the online softmax, and the weighted values are summed with lanes
+// again a pair of dimensions (a key's values one coalesced 256-byte read). The waves merge
 // through LDS into the workgroup's partial.
 template <int G>
 __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(AttentionArgs a) {
-    __shared__ float qs[G][ATT_DIM];
-    __shared__ float probs[ATT_WAVES][G][WAVE];
+    __shared__ float scores[ATT_WAVES][G][ATT_WAVE_KEYS];
     __shared__ float merge[ATT_WAVES][G][ATT_DIM + 2];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -107,58 +135,68 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
     // a slot outside the cache holds no keys; lengths past its positions stop at them
     const int length = slot >= 0 && slot < a.cache_slots ? min(a.lengths[row], a.cache_positions) : 0;
     const int h0 = kvh * G;
-    for (int i = threadIdx.x; i < G * ATT_DIM; i += ATT_WAVES * 64)
-        qs[i / ATT_DIM][i % ATT_DIM] = a.q[((int64_t)(h0 + i / ATT_DIM) * a.rows + row) * ATT_DIM + i % ATT_DIM];
-    __syncthreads();
-
+    const float qscale = a.scale * LOG2E;
+    float qa[G], qb[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float2 v = *(const float2*)(a.q + ((int64_t)(h0 + h) * a.rows + row) * ATT_DIM + 2 * lane);
+        qa[h] = v.x * qscale, qb[h] = v.y * qscale;
+    }
     const int64_t head_base = ((int64_t)slot * a.kv_heads + kvh) * a.cache_positions;  // position 0 of the head
-    const _Float16* keys = a.cache + head_base * ATT_DIM;
-    const _Float16* vals = a.cache + ((int64_t)a.cache_slots * a.kv_heads * a.cache_positions + head_base) * ATT_DIM;
+    const uint32_t* keys = (const uint32_t*)(a.cache + head_base * ATT_DIM) + lane;
+    const uint32_t* vals = (const uint32_t*)(a.cache + ((int64_t)a.cache_slots * a.kv_heads * a.cache_positions + head_base) * ATT_DIM) + lane;
+    const int last = a.cache_positions - 1;
     float m[G], l[G], acc[G][2];
 #pragma unroll
     for (int h = 0; h < G; h++) m[h] = NEG, l[h] = 0.0f, acc[h][0] = acc[h][1] = 0.0f;
 
-    for (int base = chunk * ATT_KEYS + w * WAVE; base < length; base += a.chunks * ATT_KEYS) {
-        // scores: lane = key
-        const int key = base + lane;
-        const bool valid = key < length;
-        const uint4* kp = (const uint4*)(keys + (int64_t)min(key, a.cache_positions - 1) * ATT_DIM);
-        float s[G];
+    for (int base = chunk * ATT_KEYS + w * ATT_WAVE_KEYS; base < length; base += a.chunks * ATT_KEYS) {
+        // scores of keys base .. base + 31: 16 keys at a time, lane l's share of each dot product
 #pragma unroll
-        for (int h = 0; h < G; h++) s[h] = 0.0f;
-#pragma unroll 4
-        for (int c = 0; c < ATT_DIM / 8; c++) {
-            const uint4 raw = kp[c];
-            const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+        for (int sb = 0; sb < ATT_WAVE_KEYS / 16; sb++) {
+            uint32_t kv[16];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float k0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[e] & 0xFFFFu));
-                const float k1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(words[e] >> 16));
+            for (int j = 0; j < 16; j++) kv[j] = keys[(int64_t)min(base + 16 * sb + j, last) * (ATT_DIM / 2)];
 #pragma unroll
-                for (int h = 0; h < G; h++) s[h] += qs[h][8 * c + 2 * e] * k0 + qs[h][8 * c + 2 * e + 1] * k1;
+            for (int h = 0; h < G; h++) {
+                float part[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const float k0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kv[j] & 0xFFFFu));
+                    const float k1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kv[j] >> 16));
+                    part[j] = qa[h] * k0 + qb[h] * k1;
+                }
+                const float s = transpose_sum16(part, lane);
+                if ((lane & 3) == 0) scores[w][h][16 * sb + (lane >> 2)] = s;
             }
         }
-        // the online softmax: rescale the sums by the new maximum's step
+        // the online softmax, a key a lane (lanes 32.. idle): rescale by the new maximum's step
+        const int keys_here = min(ATT_WAVE_KEYS, length - base);
+        const bool valid = lane < keys_here;
 #pragma unroll
         for (int h = 0; h < G; h++) {
-            const float sc = valid ? s[h] * a.scale : NEG;
+            const float sc = valid ? scores[w][h][lane & (ATT_WAVE_KEYS - 1)] : NEG;
             const float top = fmaxf(m[h], wave_max_dpp(sc));
-            const float p = valid ? exp2f((sc - top) * LOG2E) : 0.0f;
-            const float shrink = exp2f((m[h] - top) * LOG2E);
+            const float p = valid ? exp2f(sc - top) : 0.0f;
+            const float shrink = exp2f(m[h] - top);
             m[h] = top;
             l[h] = l[h] * shrink + wave_sum_dpp(p);
             acc[h][0] *= shrink, acc[h][1] *= shrink;
-            probs[w][h][lane] = p;
+            if (lane < ATT_WAVE_KEYS) scores[w][h][lane] = p;
         }
-        // weighted values: lane = dimensions 2 lane, 2 lane + 1; keys past the row weigh 0
-        const int keys_here = min(WAVE, length - base);
-        for (int j = 0; j < keys_here; j++) {
-            const uint32_t pair = *(const uint32_t*)(vals + (int64_t)(base + j) * ATT_DIM + 2 * lane);
-            const float v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(pair & 0xFFFFu));
-            const float v1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(pair >> 16));
+        // weighted values: lane = dimensions 2 lane, 2 lane + 1; keys past the row weigh nothing
+        uint32_t vv[ATT_WAVE_KEYS];
+#pragma unroll
+        for (int j = 0; j < ATT_WAVE_KEYS; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
+#pragma unroll
+        for (int j = 0; j < ATT_WAVE_KEYS; j++) {
+            // a position past the row's keys may hold anything, NaN included: it adds nothing
+            const bool in = j < keys_here;
+            const float v0 = in ? (float)__builtin_bit_cast(_Float16, (uint16_t)(vv[j] & 0xFFFFu)) : 0.0f;
+            const float v1 = in ? (float)__builtin_bit_cast(_Float16, (uint16_t)(vv[j] >> 16)) : 0.0f;
 #pragma unroll
             for (int h = 0; h < G; h++) {
-                const float p = probs[w][h][j];
+                const float p = scores[w][h][j];  // 0 past the row's keys
                 acc[h][0] += p * v0, acc[h][1] += p * v1;
             }
         }
@@ -182,40 +220,52 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
             y = top;
         } else {
 #pragma unroll
-            for (int v = 0; v < ATT_WAVES; v++) y += exp2f((merge[v][h][ATT_DIM] - top) * LOG2E) * merge[v][h][d];
+            for (int v = 0; v < ATT_WAVES; v++) y += exp2f(merge[v][h][ATT_DIM] - top) * merge[v][h][d];
         }
         a.partial[(((int64_t)row * a.heads + h0 + h) * a.chunks + chunk) * (ATT_DIM + 2) + d] = y;
     }
 }
 
-// A wave per (row, query head): the chunks' partials rescaled to their common maximum and
-// summed, over the sum of their weights; lane = dimensions 2 lane, 2 lane + 1
-__global__ __launch_bounds__(64) void attention_combine_kernel(AttentionArgs a) {
-    const int rh = blockIdx.x, row = rh / a.heads, lane = threadIdx.x;
+// A workgroup of ATT_COMBINE_WAVES waves per (row, query head). In every wave lane c takes chunk
+// c's max and sum (up to 64 chunks) and the wave finds the common maximum and the total weight;
+// then lane = dimensions 2 lane, 2 lane + 1, wave w sums the rescaled partials of chunks w,
+// w + ATT_COMBINE_WAVES, ..., and the waves' sums meet in LDS.
+constexpr int ATT_COMBINE_WAVES = 4;
+
+__global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kernel(AttentionArgs a) {
+    __shared__ float2 sums[ATT_COMBINE_WAVES - 1][64];
+    const int rh = blockIdx.x, row = rh / a.heads, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int slot = a.slots[row];
     const int length = slot >= 0 && slot < a.cache_slots ? min(a.lengths[row], a.cache_positions) : 0;
     const int live = min(a.chunks, (length + ATT_KEYS - 1) / ATT_KEYS);
     const float* p = a.partial + (int64_t)rh * a.chunks * (ATT_DIM + 2);
-    float top = NEG;
-    for (int c = 0; c < live; c++) top = fmaxf(top, p[c * (ATT_DIM + 2) + ATT_DIM]);
-    float y0 = 0.0f, y1 = 0.0f, total = 0.0f;
-    for (int c = 0; c < live; c++) {
-        const float* q = p + c * (ATT_DIM + 2);
-        const float f = exp2f((q[ATT_DIM] - top) * LOG2E);
-        total += f * q[ATT_DIM + 1];
-        y0 += f * q[2 * lane], y1 += f * q[2 * lane + 1];
+    const float mine = lane < live ? p[lane * (ATT_DIM + 2) + ATT_DIM] : NEG;
+    const float top = wave_max_dpp(mine);
+    const float f = lane < live ? exp2f(mine - top) : 0.0f;
+    float y0 = 0.0f, y1 = 0.0f;
+#pragma unroll 4
+    for (int c = w; c < live; c += ATT_COMBINE_WAVES) {
+        const float fc = __shfl(f, c, WAVE);
+        const float2 v = *(const float2*)(p + c * (ATT_DIM + 2) + 2 * lane);
+        y0 += fc * v.x, y1 += fc * v.y;
     }
+    if (w > 0) sums[w - 1][lane] = make_float2(y0, y1);
+    __syncthreads();
+    if (w > 0) return;
+    const float total = wave_sum_dpp(lane < live ? f * p[lane * (ATT_DIM + 2) + ATT_DIM + 1] : 0.0f);
+#pragma unroll
+    for (int v = 0; v < ATT_COMBINE_WAVES - 1; v++) y0 += sums[v][lane].x, y1 += sums[v][lane].y;
     const float inv = total > 0.0f ? 1.0f / total : 0.0f;
     float* o = a.out + (int64_t)row * a.heads * ATT_DIM + (int64_t)(rh % a.heads) * ATT_DIM;
-    o[2 * lane] = y0 * inv;
-    o[2 * lane + 1] = y1 * inv;
+    *(float2*)(o + 2 * lane) = make_float2(y0 * inv, y1 * inv);
 }
 
 template <int G>
 static int attention_go(AttentionArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attention_partial_kernel<G>), dim3(a.chunks, a.kv_heads, a.rows), dim3(ATT_WAVES * 64), 0, st, a);
     if (check_launch("attention")) return -1;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(a.rows * a.heads), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(a.rows * a.heads), dim3(ATT_COMBINE_WAVES * 64), 0, st, a);
     return check_launch("attention combine");
 }
 
