@@ -151,19 +151,23 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
     for (int h = 0; h < G; h++) m[h] = NEG, l[h] = 0.0f, acc[h][0] = acc[h][1] = 0.0f;
 
     for (int base = chunk * ATT_KEYS + w * ATT_WAVE_KEYS; base < length; base += a.chunks * ATT_KEYS) {
+        // the round's keys and values are all read at once (64 reads in flight a wave)
+        uint32_t kv[ATT_WAVE_KEYS], vv[ATT_WAVE_KEYS];
+#pragma unroll
+        for (int j = 0; j < ATT_WAVE_KEYS; j++) kv[j] = keys[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
+#pragma unroll
+        for (int j = 0; j < ATT_WAVE_KEYS; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
         // scores of keys base .. base + 31: 16 keys at a time, lane l's share of each dot product
 #pragma unroll
         for (int sb = 0; sb < ATT_WAVE_KEYS / 16; sb++) {
-            uint32_t kv[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++) kv[j] = keys[(int64_t)min(base + 16 * sb + j, last) * (ATT_DIM / 2)];
 #pragma unroll
             for (int h = 0; h < G; h++) {
                 float part[16];
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
-                    const float k0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kv[j] & 0xFFFFu));
-                    const float k1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kv[j] >> 16));
+                    const uint32_t kj = kv[16 * sb + j];
+                    const float k0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kj & 0xFFFFu));
+                    const float k1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kj >> 16));
                     part[j] = qa[h] * k0 + qb[h] * k1;
                 }
                 const float s = transpose_sum16(part, lane);
@@ -185,9 +189,6 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
             if (lane < ATT_WAVE_KEYS) scores[w][h][lane] = p;
         }
         // weighted values: lane = dimensions 2 lane, 2 lane + 1; keys past the row weigh nothing
-        uint32_t vv[ATT_WAVE_KEYS];
-#pragma unroll
-        for (int j = 0; j < ATT_WAVE_KEYS; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
 #pragma unroll
         for (int j = 0; j < ATT_WAVE_KEYS; j++) {
             // a position past the row's keys may hold anything, NaN included: it adds nothing

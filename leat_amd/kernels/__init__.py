@@ -18,6 +18,7 @@ from leat_amd import _lib
 from leat_amd.kernels.attention import (
     argmax,
     attention,
+    attention_workspace,
     embedding,
     rotate,
     supports_argmax,
@@ -493,7 +494,7 @@ def mixture(
 
 
 __all__ = [
-    "argmax", "attention", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
+    "argmax", "attention", "attention_workspace", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
     "supports_rotate",
     "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
     "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",

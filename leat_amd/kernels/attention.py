@@ -77,20 +77,36 @@ def supports_attention(q: torch.Tensor, cache: torch.Tensor) -> bool:
             and q.shape[0] == 1 and _on_gfx950(q))  # fmt: skip
 
 
+def attention_workspace(rows: int, heads: int, max_length: int, device) -> torch.Tensor:
+    """A workspace for attention() calls of up to `rows` rows of `heads` query heads and rows of at
+    most `max_length` keys, reusable by such calls one after another on a stream. Calls that may
+    overlap need workspaces of their own."""
+    size = int(_lib.lib().leat_attention_workspace(rows, heads, max_length))
+    return torch.empty(max(size, 4), dtype=torch.uint8, device=device)
+
+
 def attention(
     q: torch.Tensor, cache: torch.Tensor, slots, lengths, scale: float, max_length: int | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:  # fmt: skip
     """FlashDecoding (leat/kernels/attention.py:226-279): q (1, H, T, D), a query token a row; row t
     over the first lengths[t] positions of slot slots[t] of the cache (2, slots, KV_H, positions,
     D), scores q.k * scale. `max_length` bounds every length (the cache's positions if not
-    given) and sizes the launch. Returns (1, T, H * D) f32."""
+    given) and sizes the launch. `workspace` is one from attention_workspace() for at least these
+    rows, heads and max_length (a new one is made if not given). Returns (1, T, H * D) f32."""
     _lib.require_device(q)
     _, heads, rows, dim = q.shape
     _, cache_slots, kv_heads, cache_positions, _ = cache.shape
     device = q.device
     longest = cache_positions if max_length is None else int(max_length)
     size = int(_lib.lib().leat_attention_workspace(rows, heads, longest))
-    work = torch.empty(max(size, 4) // 4, dtype=torch.float32, device=device)
+    if workspace is None:
+        work = torch.empty(max(size, 4), dtype=torch.uint8, device=device)
+    else:
+        work = workspace
+        if work.dtype != torch.uint8 or not work.is_contiguous() or work.numel() < size or work.device != device:
+            raise _lib.LeatError("attention: the workspace is not one of attention_workspace() for these rows")
+        size = work.numel() // 4 * 4
     out = torch.empty(rows * heads * dim, dtype=torch.float32, device=device)
     src = q.float().contiguous()
     slot_rows, length_rows = _rows_tensor(slots, device), _rows_tensor(lengths, device)

@@ -195,6 +195,7 @@ class Model:
     weights: Weights
     cache: list[torch.Tensor] = field(default_factory=list)
     rope: tuple[torch.Tensor, torch.Tensor] | None = None
+    _workspaces: dict[int, torch.Tensor] = field(default_factory=dict, repr=False)
 
     def __post_init__(self):
         c = self.config
@@ -205,6 +206,16 @@ class Model:
         if self.rope is None:
             factors = None if c.rope_scaling is None else llama3_rope_factors(c.head_dim, c.rope_theta, c.rope_scaling)
             self.rope = rope_table(c.head_dim, c.rope_theta, c.context, factors, device)
+
+    def _attention_workspace(self, rows: int) -> torch.Tensor | None:
+        # one workspace for every layer's attention of a decode batch, kept for the model's
+        # life (a captured step replays with it); long prompt chunks get theirs per call
+        if rows > 64 or ops.reference_mode() or not self.weights.output.data.is_cuda:
+            return None
+        if rows not in self._workspaces:
+            c = self.config
+            self._workspaces[rows] = kernels.attention_workspace(rows, c.heads, c.context, self.weights.output.data.device)
+        return self._workspaces[rows]
 
     def logits(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
                lengths: torch.Tensor | None = None, last: bool = False) -> torch.Tensor:  # fmt: skip
@@ -225,7 +236,7 @@ class Model:
             q, k, v = ops.linears(x, layer.q, layer.k, layer.v, norm=(layer.attn_norm, c.norm_eps))
             q_rot, _ = ops.rotate(q.view(1, B, c.heads, c.head_dim), k.view(1, B, c.kv_heads, c.head_dim),
                                   v.view(1, B, c.kv_heads, c.head_dim), cache, None, rope, False, slots, positions)  # fmt: skip
-            att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context)
+            att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context, self._attention_workspace(B))
             x = ops.linear(att, layer.o, residual=x)
             x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))
         if last:

@@ -267,16 +267,17 @@ def rotate(
 
 def attention(
     q: torch.Tensor, cache: torch.Tensor, spans: list[Span] | None, scale: float, slots=None, lengths=None,
-    max_length: int | None = None,
+    max_length: int | None = None, workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:  # fmt: skip
     """q (1, H, T, D), the spans' tokens in turn, each token attending causally over its slot's
     positions up to its own, scores q.k * scale (leat/ops.py:305-339). `slots` and `lengths`
-    (device tensors, a row each) may replace the spans. Returns (1, T, H * D) f32."""
+    (device tensors, a row each) may replace the spans; `workspace` (kernels.attention_workspace)
+    is reused by the kernel path. Returns (1, T, H * D) f32."""
     if slots is None:
         slots, positions = _span_rows(spans)
         lengths = [p + 1 for p in positions]
     if not reference_mode() and kernels.supports_attention(q, cache):
-        return kernels.attention(q, cache, slots, lengths, scale, max_length)
+        return kernels.attention(q, cache, slots, lengths, scale, max_length, workspace)
     slot_list = slots.tolist() if isinstance(slots, torch.Tensor) else list(slots)
     length_list = lengths.tolist() if isinstance(lengths, torch.Tensor) else list(lengths)
     _, heads, _, dim = q.shape

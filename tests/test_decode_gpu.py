@@ -100,6 +100,24 @@ def test_attention_rows(cuda, heads, kv_heads):
         assert_close(got[t], want, 1e-4)
 
 
+def test_attention_workspace_reuse(cuda):
+    # one workspace serves calls of as many rows or fewer one after another
+    rng = np.random.default_rng(5)
+    heads, kv_heads, n = 16, 4, 2048
+    cache = rng.standard_normal((2, SLOTS, kv_heads, n, 128)).astype(np.float16)
+    device_cache = gpu(cache)
+    work = kernels.attention_workspace(4, heads, n, cuda)
+    for rows in ([(0, 2047), (1, 5), (2, 300), (0, 1000)], [(2, 129)], [(1, 0), (0, 700), (2, 2047)],
+                 [(0, 2047), (1, 127), (2, 128), (1, 1500)]):  # fmt: skip
+        q = normal(rng, 1, heads, len(rows), 128, scale=0.3)
+        slots, lengths = [s for s, _ in rows], [p + 1 for _, p in rows]
+        got = host(kernels.attention(gpu(q), device_cache, slots, lengths, 0.1, n, work))[0]
+        got = got.reshape(len(rows), heads, 128)
+        for t, (slot, pos) in enumerate(rows):
+            want = O.attention(q[0, :, t], cache[0, slot, :, : pos + 1], cache[1, slot, :, : pos + 1], 0.1)
+            np.testing.assert_allclose(got[t], want, rtol=2e-3, atol=2e-3)
+
+
 @pytest.mark.parametrize("rows, n", [(1, 128256), (5, 32000), (2, 300)])
 def test_argmax(cuda, rows, n):
     # leat's test_argmax (tests/test_kernels.py:926-933): many ties, the first must win; -inf
