@@ -51,18 +51,12 @@ __device__ __forceinline__ uint32_t minus_bytes(uint32_t q, uint32_t offset) {
     return (q + (128u - offset) * 0x01010101u) ^ 0x80808080u;
 }
 
-// a weight load. Marking them nontemporal (streamed once) measured slower on gfx950: a block's
-// bytes straddle 128-byte lines that neighbouring loads read again, and the hint evicts them first.
-#ifndef LEAT_NONTEMPORAL
-#define LEAT_NONTEMPORAL 0
-#endif
+// a weight load: a plain one. Marking them nontemporal (streamed once) measured slower on gfx950:
+// a block's bytes straddle 128-byte lines that neighbouring loads read again, and the hint evicts
+// them first.
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
-#if LEAT_NONTEMPORAL
-    return __builtin_nontemporal_load(p);
-#else
     return *p;
-#endif
 }
 
 // 16 bytes at a byte offset that is even but maybe not 4-aligned: 5 aligned dwords, realigned

@@ -197,10 +197,8 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // 4. each wave streams 4 rows of gate and up against the members' activations in registers;
 // 5. the 32 rows are one group of 32 per pair, so the workgroup writes the hidden rows' q8 words,
 //    d and s as well as (optionally) their f32 values.
-#ifndef LEAT_MOE_WAVES
-#define LEAT_MOE_WAVES 8  // waves of a workgroup: 32 rows, 32 / LEAT_MOE_WAVES a wave (16 spill)
-#endif
-constexpr int MOE_WAVES = LEAT_MOE_WAVES, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
+// MOE_WAVES waves of a workgroup: 32 rows, 4 a wave (16 waves spill registers)
+constexpr int MOE_WAVES = 8, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
 
 struct MoeGluArgs {
     const uint8_t* gate;

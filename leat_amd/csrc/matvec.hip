@@ -143,9 +143,7 @@ constexpr int rows_per_wave() {
     return MODE == MODE_GLU ? 1 : (B <= 8 ? 2 : 1);
 }
 
-#ifndef LEAT_MATVEC_UNROLL
-#define LEAT_MATVEC_UNROLL 2
-#endif
+constexpr int MATVEC_UNROLL = 2;  // one token's rows: tasks a lane has in flight
 
 template <int TYPE, int B, int MODE>
 static int launch_b(MatvecArgs& a, hipStream_t stream) {
@@ -161,7 +159,7 @@ static int launch_b(MatvecArgs& a, hipStream_t stream) {
     // two rows a wave, measured faster reading them from L2
     const size_t lds = (size_t)B * (a.cols + a.cols / GROUP * 8);
     if (MODE != MODE_GLU && B <= 2 && lds <= 40960) {
-        constexpr int U = B == 1 ? LEAT_MATVEC_UNROLL : 1;
+        constexpr int U = B == 1 ? MATVEC_UNROLL : 1;
         hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE, U, true>), dim3(blocks), dim3(256), lds, stream, a);
     } else {
         hipLaunchKernelGGL((matvec_kernel<TYPE, B, R, MODE, 1, false>), dim3(blocks), dim3(256), 0, stream, a);
@@ -199,12 +197,7 @@ static int launch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     }
 }
 
-#ifndef LEAT_MMV_MIN_TOKENS
-#define LEAT_MMV_MIN_TOKENS 3  // the fewest tokens the matrix-core path takes
-#endif
-#ifndef LEAT_TILES
-#define LEAT_TILES 1  // 0: 3..8 tokens take the staged matrix-core kernels instead of the tile kernels
-#endif
+constexpr int MMV_MIN_TOKENS = 3;  // the fewest tokens the matrix-core path takes
 
 // one or two tokens: the row-streaming kernels; 3..8: the matrix-core tile kernels for the GLU,
 // the staged matrix-core kernels (mmv) for the rest; more (16): the staged ones where they fit
@@ -229,7 +222,7 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
     }
     // 3..8 tokens: the GLU on the tile kernels; the plain and residual products (where they fit)
     // on the staged ones, which measured faster for them
-    if (LEAT_TILES && tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw) &&
+    if (tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw) &&
         (MODE == MODE_GLU || !mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw))) {
         TileArgs t = {};
         for (int i = 0; i < MAX_MATS; i++) {
@@ -246,7 +239,7 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         t.hq = a.hq, t.hd = a.hd, t.hs = a.hs;
         return tiles_launch(type, MODE, t, s);
     }
-    if (tokens >= LEAT_MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
+    if (tokens >= MMV_MIN_TOKENS && mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw)) {
         MmvArgs m = {};
         for (int i = 0; i < MAX_MATS; i++) {
             m.w[i] = a.w[i];
@@ -340,7 +333,7 @@ extern "C" int leat_matvec(int type, const void* w, int rows, int cols, const in
 // multiple of 32): the row-streaming kernels (1..2 tokens) and the tile kernels (3..8 of Q4_K)
 static bool glu_q8_inside(int type, int cols, int tokens, const void* gate, const void* up) {
     const void* ws[2] = {gate, up};
-    return rows_fits(type, cols, tokens, true) || (LEAT_TILES && tiles_fits(type, cols, tokens, ws, 2));
+    return rows_fits(type, cols, tokens, true) || tiles_fits(type, cols, tokens, ws, 2);
 }
 
 extern "C" int leat_glu_matvec_q8(int type, const void* gate, const void* up, int rows, int cols, const int32_t* xq,

@@ -343,21 +343,13 @@ struct Compute<Q8_0> {
     }
 };
 
-#ifndef LEAT_MMV_DEPTH
-#define LEAT_MMV_DEPTH 1  // stages of loads a wave keeps in flight (1 or 2)
-#endif
-#ifndef LEAT_MMV_INTERLEAVE
-#define LEAT_MMV_INTERLEAVE 1  // the waves of a tile take every S-th stage (else runs of stages)
-#endif
+constexpr int MMV_DEPTH = 1;  // stages of loads a wave keeps in flight besides the one it computes
 
 // waves per SIMD the register budget allows: 4 (128 registers) for one Q4_K or Q8_0 matrix and
 // up to two tokens' results, 3 (168) for Q6_K's wider stages, else 2 (256). A wave keeps a stage
 // of its tile in flight, so a few waves per SIMD cover HBM's latency.
-#ifndef LEAT_MMV_GLU_OCC
-#define LEAT_MMV_GLU_OCC 2
-#endif
 constexpr int mmv_occupancy(int type, int mode, int nv) {
-    return mode == MMV_GLU && nv > 2 ? LEAT_MMV_GLU_OCC : mode == MMV_GLU || nv > 2 ? 2 : type == Q6_K ? 3 : 4;
+    return mode == MMV_GLU || nv > 2 ? 2 : type == Q6_K ? 3 : 4;
 }
 
 template <int TYPE>
@@ -397,17 +389,13 @@ void mmv_kernel(MmvArgs args) {
     // the wave's stages, and the first one's loads before anything else
     const int stages = nb / G::BPS;
     const int p0 = stages * part / args.parts, pn = stages * (part + 1) / args.parts - p0;
-    // the wave's stages ka + ks j, j < nk: with LEAT_MMV_INTERLEAVE every S-th of the part's
-    // (the S waves read neighbouring blocks of the tile's rows at a time), else a run of them
-#if LEAT_MMV_INTERLEAVE
+    // the wave's stages ka + ks j, j < nk: every S-th of the part's, so the S waves read
+    // neighbouring blocks of the tile's rows at a time
     const int ka = p0 + wave, ks = S, nk = ka < p0 + pn ? (p0 + pn - ka + S - 1) / S : 0;
-#else
-    const int ka = p0 + pn * wave / S, ks = 1, nk = p0 + pn * (wave + 1) / S - ka;
-#endif
-    // stages j and (LEAT_MMV_DEPTH 2) j + 1 in flight
-    Stage<TYPE> st[LEAT_MMV_DEPTH][NM];
+    // MMV_DEPTH stages in flight
+    Stage<TYPE> st[MMV_DEPTH][NM];
 #pragma unroll
-    for (int p = 0; p < LEAT_MMV_DEPTH; p++)
+    for (int p = 0; p < MMV_DEPTH; p++)
         if (p < nk)
 #pragma unroll
             for (int i = 0; i < NM; i++) stage_load<TYPE>(st[p][i], wm[i], row_bytes, row0, rows, ka + ks * p, lane);
@@ -476,13 +464,13 @@ void mmv_kernel(MmvArgs args) {
 
     constexpr int GS = TYPE == Q8_0 ? 2 : 8;  // groups a stage
     if (A::SETS == 2 && nk > 0) acts.template load<GS>(0, ka * GS);
-    constexpr int UNR = A::SETS == 2 ? 2 : LEAT_MMV_DEPTH;  // stages a loop turn: the sets alternate
+    constexpr int UNR = A::SETS == 2 ? 2 : MMV_DEPTH;  // stages a loop turn: the sets alternate
     for (int j0 = 0; j0 < nk; j0 += UNR) {
 #pragma unroll
         for (int p = 0; p < UNR; p++) {
             // stage j: its registers go to the wave's LDS region and take the loads of stage
             // j + DEPTH; its activation operands are set p, the next stage's go to set 1 - p
-            const int sp = p % LEAT_MMV_DEPTH, j = j0 + p, k = ka + ks * j;
+            const int sp = p % MMV_DEPTH, j = j0 + p, k = ka + ks * j;
             if (j >= nk) break;
             // (the last stage loads its own set again: no branch around loads, as above)
             if (A::SETS == 1)
@@ -496,7 +484,7 @@ void mmv_kernel(MmvArgs args) {
             for (int i = 0; i < NM; i++) stage_store<TYPE>(st[sp][i], regions + (wave * NM + i) * 32 * G::RS, lane);
 #pragma unroll
             for (int i = 0; i < NM; i++)  // (past the last stage: the last again, never stored)
-                stage_load<TYPE>(st[sp][i], wm[i], row_bytes, row0, rows, ka + ks * min(j + LEAT_MMV_DEPTH, nk - 1), lane);
+                stage_load<TYPE>(st[sp][i], wm[i], row_bytes, row0, rows, ka + ks * min(j + MMV_DEPTH, nk - 1), lane);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -551,15 +539,7 @@ __global__ void mmv_zero(MmvArgs a) {
         a.out[m][i] = 0.0f;
 }
 
-#ifndef LEAT_MMV_S16
-#define LEAT_MMV_S16 0
-#endif
-#ifndef LEAT_MMV_SPLIT_STAGES
-#define LEAT_MMV_SPLIT_STAGES 32  // the fewest stages (blocks) a row needs for the split
-#endif
-#ifndef LEAT_MMV_KSPLIT
-#define LEAT_MMV_KSPLIT 1  // split the blocks of tiles over two workgroups when tiles are fewer than CUs
-#endif
+constexpr int MMV_SPLIT_STAGES = 32;  // the fewest stages (blocks) a row needs to split it over two workgroups
 
 // the current device's CU count, read once per device; callers on several threads may race to
 // fill an entry, and all store the same value
@@ -575,9 +555,7 @@ int cu_count() {
     }
     return known;
 }
-#ifndef LEAT_MMV_WAVES
-#define LEAT_MMV_WAVES 4096  // waves a launch aims for: 16 per CU
-#endif
+constexpr int MMV_WAVES = 4096;  // waves a launch aims for: 16 per CU
 
 template <int TYPE, int MODE, int NV, int S>
 static int mmv_launch_s(MmvArgs& a, hipStream_t st) {
@@ -609,18 +587,12 @@ static int mmv_launch_nv(MmvArgs& a, hipStream_t st) {
     // (not when the output is the residual itself: zeroing it first would lose the residual)
     const size_t n = (size_t)a.tokens * a.rows[0];
     const bool in_place = MODE == MMV_RESIDUAL && a.residual < a.out[0] + n && a.out[0] < a.residual + n;
-    a.parts = LEAT_MMV_KSPLIT && MODE != MMV_GLU && !in_place && a.tile_start[a.count] < cu_count() &&
-                      stages >= LEAT_MMV_SPLIT_STAGES
+    a.parts = MODE != MMV_GLU && !in_place && a.tile_start[a.count] < cu_count() && stages >= MMV_SPLIT_STAGES
                   ? 2
                   : 1;
     const int tiles = a.tile_start[a.count] * a.parts;
     // waves per tile: enough for the launch to fill the GPU, at most one per stage of a row
-    const int want = (LEAT_MMV_WAVES + tiles - 1) / tiles;
-#if LEAT_MMV_S16
-    // few tiles (a 4096-row down product: 128): 16 waves a tile keep enough bytes in flight
-    if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1 && MODE != MMV_GLU && NV <= 4)
-        if (want >= 16 && stages >= 16) return mmv_launch_s<TYPE, MODE, NV, 16>(a, st);
-#endif
+    const int want = (MMV_WAVES + tiles - 1) / tiles;
     if constexpr (mmv_occupancy(TYPE, MODE, NV) > 1)
         if (want >= 8 && stages >= 8) return mmv_launch_s<TYPE, MODE, NV, 8>(a, st);
     if (want >= 4 && stages >= 4) return mmv_launch_s<TYPE, MODE, NV, 4>(a, st);

@@ -27,13 +27,7 @@ namespace leat {
 
 enum RowsMode : int { ROWS_PLAIN = 0, ROWS_RESIDUAL = 1, ROWS_GLU = 2 };
 
-#ifndef LEAT_ROWS_INTERLEAVE
-#define LEAT_ROWS_INTERLEAVE 1
-#endif
-
-#ifndef LEAT_ROWS_DEPTH
-#define LEAT_ROWS_DEPTH 1  // rows of weight loads a wave has in flight, the one it computes next included
-#endif
+constexpr int ROWS_DEPTH = 1;  // rows of weight loads a wave has in flight, the one it computes next included
 
 // FULL: the row's tasks fill exactly NT turns of the wave, so no lane needs a bounds check
 // WPG waves per workgroup, RPW rows per wave: a workgroup owns a tile of WPG * RPW rows
@@ -49,9 +43,8 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     const int cols = a.cols, tasks = cols / T::TASK_W;
     const int lane = threadIdx.x & (WAVE - 1);
     // the wave's number in the workgroup, known to the compiler as uniform so row addresses stay
-    // scalar. A workgroup owns a tile of WPG * RPW consecutive rows of one matrix; with
-    // LEAT_ROWS_INTERLEAVE its waves take every WPG-th row (w, w + WPG, ...), so at each step the
-    // waves read adjacent rows, else each wave RPW consecutive rows
+    // scalar. A workgroup owns a tile of WPG * RPW consecutive rows of one matrix; its waves take
+    // every WPG-th row (w, w + WPG, ...), so at each step the waves read adjacent rows
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int tile = blockIdx.x;
     int m = 0;
@@ -59,8 +52,8 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
         while (m + 1 < a.count && tile >= a.tile_start[m + 1]) m++;
     const int rows = a.rows[m];
     const int tile_row = (tile - a.tile_start[m]) * WPG * RPW;
-    constexpr int STEP = LEAT_ROWS_INTERLEAVE ? WPG : 1;
-    const int row0 = tile_row + (LEAT_ROWS_INTERLEAVE ? w : RPW * w);
+    constexpr int STEP = WPG;
+    const int row0 = tile_row + w;
     const uint32_t row_bytes = (uint32_t)(cols / T::WEIGHTS) * T::BYTES;
     const uint8_t* wm[NM];
     wm[0] = a.w[MODE == ROWS_GLU ? 0 : m];
@@ -74,7 +67,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     for (int i = 0; i < NT; i++) has[i] = FULL || lane + WAVE * i < tasks;
 
     // P rows' weights in flight at a time, the first P before the activations are ready
-    constexpr int P = RPW < LEAT_ROWS_DEPTH ? RPW : LEAT_ROWS_DEPTH;
+    constexpr int P = RPW < ROWS_DEPTH ? RPW : ROWS_DEPTH;
     typename RT::Raw buf[P][NM][NT];
     auto fetch = [&](typename RT::Raw(&dst)[NM][NT], int row) {
 #pragma unroll
@@ -168,9 +161,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
-#ifndef LEAT_ROWS_SPLIT_P
-#define LEAT_ROWS_SPLIT_P 2  // rows of loads a wave has in flight when long rows are split by columns
-#endif
+constexpr int ROWS_SPLIT_P = 2;  // rows of loads a wave has in flight when long rows are split by columns
 
 // Long rows (more than 4 turns of a wave's tasks: Q6_K or Q4_K rows of 14336 weights, 7 turns)
 // split by columns: wave w of the KS waves of a workgroup takes turn w of every row, tasks
@@ -179,7 +170,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
 template <int TYPE, int B, int KS, int R, int MODE>
 __global__ __launch_bounds__(KS * 64) void rows_split_kernel(RowsArgs a) {
     using RT = RowTask<TYPE>;
-    constexpr int P = R < LEAT_ROWS_SPLIT_P ? R : LEAT_ROWS_SPLIT_P;
+    constexpr int P = R < ROWS_SPLIT_P ? R : ROWS_SPLIT_P;
     __shared__ float part[KS][B][R];
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -245,23 +236,15 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
     return check_launch("rows");
 }
 
-#ifndef LEAT_ROWS_RPW
-#define LEAT_ROWS_RPW 2  // rows a wave streams in the plain and residual products
-#endif
-#ifndef LEAT_ROWS_WPG
-#define LEAT_ROWS_WPG 8  // waves per workgroup in the plain and residual products
-#endif
-#ifndef LEAT_ROWS_SPLIT_R
-#define LEAT_ROWS_SPLIT_R 2  // rows a workgroup streams when long rows are split by columns (more, fewer workgroups: slower)
-#endif
-#ifndef LEAT_ROWS_GLU_WPG
-#define LEAT_ROWS_GLU_WPG 8  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
-#endif
+constexpr int ROWS_RPW = 2;      // rows a wave streams in the plain and residual products
+constexpr int ROWS_WPG = 8;      // waves per workgroup in the plain and residual products
+constexpr int ROWS_SPLIT_R = 2;  // rows a workgroup streams when long rows are split by columns (more, fewer workgroups: slower)
+constexpr int ROWS_GLU_WPG = 8;  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
 
 template <int TYPE, int B, int NT, int MODE>
 static int rows_shape(RowsArgs& a, bool xf32, hipStream_t st) {
-    constexpr int WPG = MODE == ROWS_GLU ? LEAT_ROWS_GLU_WPG : LEAT_ROWS_WPG;
-    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : LEAT_ROWS_RPW;
+    constexpr int WPG = MODE == ROWS_GLU ? ROWS_GLU_WPG : ROWS_WPG;
+    constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : ROWS_RPW;
     return xf32 ? rows_go<TYPE, B, NT, RPW, WPG, MODE, true>(a, st) : rows_go<TYPE, B, NT, RPW, WPG, MODE, false>(a, st);
 }
 
@@ -279,7 +262,7 @@ static int rows_nt(RowsArgs& a, bool xf32, hipStream_t st) {
                 set_error("rows: long rows of %d tasks take quantized input, 7 turns", tasks);
                 return -1;
             }
-            constexpr int R = LEAT_ROWS_SPLIT_R;
+            constexpr int R = ROWS_SPLIT_R;
             RowsArgs one = a;
             for (int i = 0; i < a.count; i++) {  // a launch per matrix
                 one.w[0] = a.w[i], one.out[0] = a.out[i], one.rows[0] = a.rows[i];
@@ -299,9 +282,6 @@ static int rows_b(RowsArgs& a, int tokens, bool xf32, hipStream_t st) {
 }
 
 bool rows_fits(int type, int cols, int tokens, bool glu) {
-#ifdef LEAT_ROWS_OFF  // build without the row-streaming path (for comparisons)
-    return false;
-#endif
     if (tokens < 1 || tokens > ROWS_MAX_TOKENS) return false;
     // rows of 7 turns of a wave's 32-weight tasks (14336 weights), split by columns: q8 input, no GLU
     const bool split = !glu && cols == 7 * WAVE * 32;

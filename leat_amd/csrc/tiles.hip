@@ -257,9 +257,7 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
 
 // ------------------------------------------------------------------------------- launching
 
-#ifndef LEAT_TILES_WAVES
-#define LEAT_TILES_WAVES 2048  // waves a launch aims for
-#endif
+constexpr int TILES_WAVES = 2048;  // waves a launch aims for
 
 template <int TYPE, int MODE, int S>
 static int tiles_go(TileArgs& a, hipStream_t st) {
@@ -285,7 +283,7 @@ static int tiles_s(TileArgs& a, hipStream_t st) {
     const int tiles = a.tile_start[a.count];
     const int blocks = a.cols / 256;
     // waves per tile: enough for the launch to fill the GPU, a few blocks each
-    const int want = (LEAT_TILES_WAVES + tiles - 1) / tiles;
+    const int want = (TILES_WAVES + tiles - 1) / tiles;
     // (16 waves fit 1024 threads' 128 registers a lane only for the plain products)
     if constexpr (MODE != TILES_GLU)
         if (want >= 16 && blocks >= 32) return tiles_go<TYPE, MODE, 16>(a, st);
