@@ -229,12 +229,38 @@ TRAFFIC_SOURCES = ["blocks.h", "common.h", "q8.h", "rows.h", "rows.hip", "rowtas
                    "mmv.h", "mmv.hip", "matvec.hip"]  # fmt: skip
 
 
-def sources_sha() -> str:
-    """A digest of the decode kernels' sources, which the traffic profile records beside its bytes."""
+# the prefill kernels' sources, whose counters profiles/prefill_counters.md records
+COUNTER_PROFILE = ROOT / "profiles" / "prefill_counters.md"
+COUNTER_SOURCES = ["blocks.h", "common.h", "formats.h", "lds.h", "prefill.h", "prefill.hip", "prefill6.hip", "q8.h",
+                   "tasks.h"]  # fmt: skip
+
+
+def sources_sha(names=None) -> str:
+    """A digest of kernel sources (the decode kernels' by default), which a profile records beside
+    its figures."""
     digest = hashlib.sha256()
-    for name in TRAFFIC_SOURCES:
+    for name in TRAFFIC_SOURCES if names is None else names:
         digest.update((ROOT / "leat_amd" / "csrc" / name).read_bytes())
     return digest.hexdigest()[:16]
+
+
+def profiled_counters(kernel: str) -> dict | None:
+    """MFMA and VALU busy fractions of `kernel` as the committed rocprofv3 --pmc summary records
+    them ("counters <kernel> mfma_util=.. valu_busy=.. coexec=.."), with their source; None when
+    it has no line for the kernel or was measured on other kernel sources."""
+    try:
+        text = COUNTER_PROFILE.read_text()
+    except OSError:
+        return None
+    sha = sources_sha(COUNTER_SOURCES)
+    m = re.search(r"^sources sha ([0-9a-f]+)$", text, re.M)
+    if not m or m.group(1) != sha:
+        return None
+    m = re.search(r"^counters " + re.escape(kernel) + r" (.*)$", text, re.M)
+    if not m:
+        return None
+    fields = dict(item.split("=") for item in m.group(1).split())
+    return {**{k: float(v) for k, v in fields.items()}, "source": f"profiles/{COUNTER_PROFILE.name}, sources sha {sha}"}
 
 
 def profiled_traffic(kernel: str) -> tuple[int | None, str]:
@@ -441,6 +467,9 @@ def measure_prefill(torch, lib, w, reps, device):
                      "frac": glu_tops / INT8_PEAK_TOPS, "traffic": None,
                      "kernel": "gate+up GLU matmul (MMQ) with q8 output, Q4_K 2x14336x4096, 512 tokens",
                      "ops_per_launch": glu_ops},
+        # matrix-core and VALU busy fractions from rocprofv3 counters (what bounds each kernel)
+        "counters": {"glu": profiled_counters("prefill_q4k_glu_q8_512"),
+                     "down": profiled_counters("prefill_q6k_residual_512")},
     }  # fmt: skip
 
 

@@ -42,32 +42,31 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: Path, defines: tuple[str, ...] = (), obj_dir: Path = OBJ) -> Path:
-    obj = obj_dir / (src.stem + ".o")
-    cmd = [hipcc(), *FLAGS, *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path) -> Path:
+    obj = OBJ / (src.stem + ".o")
+    cmd = [hipcc(), *FLAGS, "-c", str(src), "-o", str(obj)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"compiling {src.name} failed:\n{done.stderr}")
     return obj
 
 
-def build(verbose: bool = False, defines: tuple[str, ...] = (), lib: Path = LIB, obj_dir: Path = OBJ) -> Path:
-    """Compiles every kernel source for gfx950 and links libleatmi.so; returns its path.
-    `defines` set compile-time tunables (NAME=VALUE) for a library built elsewhere (`lib`)."""
-    obj_dir.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = False) -> Path:
+    """Compiles every kernel source for gfx950 and links libleatmi.so; returns its path."""
+    OBJ.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(lambda src: _compile(src, tuple(defines), obj_dir), sources))
-    tmp = lib.with_suffix(".so.tmp")
+        objs = list(pool.map(_compile, sources))
+    tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     done = subprocess.run(cmd, capture_output=True, text=True)
     if done.returncode != 0:
         raise RuntimeError(f"linking libleatmi.so failed:\n{done.stderr}")
-    os.replace(tmp, lib)
+    os.replace(tmp, LIB)
     if verbose:
-        print(f"built {lib}", file=sys.stderr)
-    return lib
+        print(f"built {LIB}", file=sys.stderr)
+    return LIB
 
 
 if __name__ == "__main__":
