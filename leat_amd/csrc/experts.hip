@@ -184,20 +184,20 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 
 // The first steps of a decode mixture in one launch (leat/kernels/experts.py:341-377: route,
 // quantize_q8 of rms_norm(x), experts_swiglu, quantize_q8 of the hidden rows). A workgroup owns
-// 32 rows of the expert of pair p = blockIdx.y:
-// 1. its 8 waves route every token (route_token, the routing kernel's arithmetic) into LDS, and
+// 32 rows of the expert of pair p = blockIdx.y (token p / used), so an expert chosen by k tokens
+// is read k times: each pair's rows are streamed by workgroups of their own, which lets more
+// of them run at once than sharing a pass between members does.
+// 1. threads 0..255 load the token's x (and the norm weight) into registers before anything
+//    else, so that its norm and quantization never wait behind the weight loads;
+// 2. its 8 waves route every token (route_token, the routing kernel's arithmetic) into LDS, and
 //    workgroup (0, 0) publishes ids and weights for the down product;
-// 2. the pairs routed to one expert (at most one a token) are served C at a time, by the
-//    workgroups of the first, (C+1)-th, ... of them; the others exit. Launches take C = 1: an
-//    expert chosen by k tokens is read k times, but the workgroups' smaller register budget lets
-//    more of them run at once (8 tokens: 39 us a layer's launch against 45 with C = 2, 61 with 4);
 // 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
-//    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes the
-//    member tokens' x into LDS with the standalone quantizer's arithmetic (q8.h);
-// 4. each wave streams 4 rows of gate and up against the members' activations in registers;
-// 5. the 32 rows are one group of 32 per pair, so the workgroup writes the hidden rows' q8 words,
-//    d and s as well as (optionally) their f32 values.
-// MOE_WAVES waves of a workgroup: 32 rows, 4 a wave (16 waves spill registers)
+//    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes x into
+//    LDS with the standalone quantizer's arithmetic (q8.h);
+// 4. each wave streams 4 rows of gate and up against the activations in registers;
+// 5. the 32 rows are one group of 32, so the workgroup writes the hidden rows' q8 words, d and s
+//    as well as (optionally) their f32 values.
+// MOE_WAVES waves of a workgroup: 32 rows, 4 a wave
 constexpr int MOE_WAVES = 8, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
 
 struct MoeGluArgs {
@@ -221,24 +221,31 @@ struct MoeGluArgs {
     float* hs;
 };
 
-template <int TYPE, int NT, int C, int EPL>
+template <int TYPE, int NT, int EPL>
 __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     using RT = RowTask<TYPE>;
     constexpr int RPW = MOE_TILE / MOE_WAVES;
     constexpr int P = NT == 1 ? RPW : NT == 2 ? 2 : 1;  // rows of loads in flight
-    static_assert(NT * C <= 8, "members' activations in registers");
-    extern __shared__ uint32_t moe_lds[];  // the C member tokens' q8 rows: words, then d, then s
+    extern __shared__ uint32_t moe_lds[];  // the token's q8 row: words, then d, then s
     __shared__ int route_id[MOE_MAX_TOKENS * MOE_MAX_USED];
     __shared__ float route_w[MOE_MAX_TOKENS * MOE_MAX_USED];
     __shared__ float partial[MOE_WAVES];
-    __shared__ float glu_out[C][MOE_TILE];
+    __shared__ float glu_out[MOE_TILE];
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int p = blockIdx.y, row_base = blockIdx.x * MOE_TILE;
     const int cols = a.cols, used = a.used, pairs = a.tokens * used;
 
-    // 1. routing
+    // 1. the token's x, first in every wave's queue of loads (up to 8192 values: longer rows
+    // would spill the registers, and load theirs after the weights)
+    constexpr int NX = NT * Task<TYPE>::TASK_W / 16;
+    constexpr bool EARLY_X = NX <= 8;
+    const float* xr = a.x + (int64_t)(p / used) * cols;
+    RowsInRegs<1, EARLY_X ? NX : 1> xin;
+    if (EARLY_X) xin.load(xr, a.norm, cols);
+
+    // 2. routing
     for (int t = w; t < a.tokens; t += MOE_WAVES) {
         int id;
         float weight;
@@ -248,36 +255,9 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     __syncthreads();
     if (blockIdx.x == 0 && p == 0)
         for (int i = threadIdx.x; i < pairs; i += MOE_WAVES * 64) a.ids[i] = route_id[i], a.weights[i] = route_w[i];
-
-    // 2. the expert of pair p, and its members (the same in every wave): each lane tests one pair
-    // of a run of 64, and a wave-wide ballot counts and finds them
     const int e = route_id[p];  // route_token ids are always below `experts`
-    int rank = 0;  // the pairs before p routed to e
-    int m[C], n = 0;  // p and the next C - 1 pairs routed to e (at most one a token)
-#pragma unroll
-    for (int j = 0; j < C; j++) m[j] = p;
-    for (int base = 0; base < pairs && n < C; base += WAVE) {
-        uint64_t hit = __ballot(base + lane < pairs && route_id[base + lane] == e);
-        if (base + WAVE <= p) {
-            rank += __popcll(hit);
-            continue;
-        }
-        if (base <= p) {  // p's run: the pairs before p, then p and those after
-            const uint64_t before = (1ull << (p - base)) - 1;
-            rank += __popcll(hit & before);
-            hit &= ~before;
-        }
-        for (; hit && n < C; hit &= hit - 1) {
-            const int q = base + __ffsll((unsigned long long)hit) - 1;
-#pragma unroll
-            for (int j = 0; j < C; j++)  // m[n] = q without indexing registers at run time
-                if (j == n) m[j] = q;
-            n++;
-        }
-    }
-    if (rank % C != 0) return;  // the whole workgroup: an earlier pair's workgroup serves p
 
-    // 3. the rows' loads, then the members' activations
+    // 3. the rows' loads, then the token's activations
     const int row0 = row_base + w;  // the wave's rows: row0 + 8r
     const uint32_t row_bytes = (uint32_t)(cols / Task<TYPE>::WEIGHTS) * Task<TYPE>::BYTES;
     const typename RT::Off off = RT::at(lane);
@@ -299,64 +279,45 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     };
 #pragma unroll
     for (int r = 0; r < P; r++) fetch(r, r);
-    const int words = C * (cols / 4), groups = C * (cols / GROUP);
-    float* lds_d = (float*)(moe_lds + words);
-#pragma unroll
-    for (int j = 0; j < C; j++) {
-        if (j >= n) break;  // uniform
-        const float* xr = a.x + (int64_t)(m[j] / used) * cols;
+    float* lds_d = (float*)(moe_lds + cols / 4);
+    if constexpr (EARLY_X) {
+        xin.template quantize<MOE_WAVES * 64>(0, a.norm, a.eps, cols, partial, moe_lds, lds_d, lds_d + cols / GROUP);
+    } else {
         const float inv = a.norm ? block_inv_rms<MOE_WAVES * 64>(xr, cols, a.eps, partial) : 1.0f;
-        quantize_row<MOE_WAVES * 64>(xr, cols, a.norm, inv, moe_lds + j * (cols / 4), lds_d + j * (cols / GROUP),
-                                     lds_d + groups + j * (cols / GROUP));
+        quantize_row<MOE_WAVES * 64>(xr, cols, a.norm, inv, moe_lds, lds_d, lds_d + cols / GROUP);
     }
     __syncthreads();
-    ActQ act[NT][C];
+    ActQ act[NT];
 #pragma unroll
-    for (int i = 0; i < NT; i++)
-#pragma unroll
-        for (int j = 0; j < C; j++)
-            act[i][j] = RT::act(load_act_lds<TYPE>(moe_lds, C, cols, j < n ? j : 0, has[i] ? lane + WAVE * i : 0), lane);
+    for (int i = 0; i < NT; i++) act[i] = RT::act(load_act_lds<TYPE>(moe_lds, 1, cols, 0, has[i] ? lane + WAVE * i : 0), lane);
 
     // 4. the rows
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
         const int row = row0 + MOE_WAVES * r;
-        float g[C], u[C];
+        float g = 0.0f, u = 0.0f;
 #pragma unroll
-        for (int j = 0; j < C; j++) {
-            g[j] = u[j] = 0.0f;
-            if (j >= n) continue;  // uniform: the expert serves n of the C slots
-#pragma unroll
-            for (int i = 0; i < NT; i++)
-                if (has[i]) {
-                    g[j] += RT::dot(rg[r % P][i], off, act[i][j]);
-                    u[j] += RT::dot(ru[r % P][i], off, act[i][j]);
-                }
-        }
+        for (int i = 0; i < NT; i++)
+            if (has[i]) {
+                g += RT::dot(rg[r % P][i], off, act[i]);
+                u += RT::dot(ru[r % P][i], off, act[i]);
+            }
         if (r + P < RPW) fetch(r % P, r + P);
         const float gb = a.gate_bias && row < a.rows ? a.gate_bias[(int64_t)e * a.rows + row] : 0.0f;
         const float ub = a.up_bias && row < a.rows ? a.up_bias[(int64_t)e * a.rows + row] : 0.0f;
-#pragma unroll
-        for (int j = 0; j < C; j++) {
-            if (j >= n) break;  // uniform
-            const float y = glu(a.kind, wave_sum_dpp(g[j]) + gb, wave_sum_dpp(u[j]) + ub);
-            if (lane == 0) {
-                glu_out[j][w + MOE_WAVES * r] = y;
-                if (a.out && row < a.rows) a.out[(int64_t)m[j] * a.rows + row] = y;
-            }
+        const float y = glu(a.kind, wave_sum_dpp(g) + gb, wave_sum_dpp(u) + ub);
+        if (lane == 0) {
+            glu_out[w + MOE_WAVES * r] = y;
+            if (a.out && row < a.rows) a.out[(int64_t)p * a.rows + row] = y;
         }
     }
 
-    // 5. each member's 32 outputs quantized as one group (rows a multiple of 32)
+    // 5. the 32 outputs quantized as one group (rows a multiple of 32)
     if (!a.hq) return;
     __syncthreads();
-    if ((int)threadIdx.x < MOE_TILE * C) {
-        const int j = threadIdx.x / MOE_TILE, i = threadIdx.x % MOE_TILE;
-        int mj = m[0];
-#pragma unroll
-        for (int k = 1; k < C; k++)
-            if (k == j) mj = m[k];
-        const float v = glu_out[j][i];
+    if ((int)threadIdx.x < MOE_TILE) {
+        const int i = threadIdx.x;
+        const float v = glu_out[i];
         float amax = fabsf(v);
 #pragma unroll
         for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
@@ -369,42 +330,34 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
         const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
         const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
         const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
-        if (j < n) {
-            const int64_t first = (int64_t)mj * a.rows + row_base;
-            if ((i & 3) == 0) a.hq[(first + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            if (i == 0) {
-                a.hd[first / GROUP] = scale;
-                a.hs[first / GROUP] = scale * (float)total;
-            }
+        const int64_t first = (int64_t)p * a.rows + row_base;
+        if ((i & 3) == 0) a.hq[(first + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        if (i == 0) {
+            a.hd[first / GROUP] = scale;
+            a.hs[first / GROUP] = scale * (float)total;
         }
     }
 }
 
-template <int TYPE, int NT, int C>
+template <int TYPE, int NT>
 static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
     const dim3 grid((a.rows + MOE_TILE - 1) / MOE_TILE, a.tokens * a.used);
-    const size_t lds = (size_t)C * a.cols + 2 * (size_t)C * (a.cols / GROUP) * 4;
+    const size_t lds = (size_t)a.cols + 2 * (size_t)(a.cols / GROUP) * 4;
     if (a.experts <= WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 1>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 1>), grid, dim3(MOE_WAVES * 64), lds, st, a);
     else if (a.experts <= 2 * WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 2>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 2>), grid, dim3(MOE_WAVES * 64), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, C, 4>), grid, dim3(MOE_WAVES * 64), lds, st, a);
-}
-
-// one member slot a pass (C = 1): faster than sharing an expert's rows between members
-template <int TYPE, int NT>
-static void moe_glu_c(MoeGluArgs& a, hipStream_t st) {
-    moe_glu_go<TYPE, NT, 1>(a, st);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 4>), grid, dim3(MOE_WAVES * 64), lds, st, a);
 }
 
 template <int TYPE>
 static void moe_glu_nt(MoeGluArgs& a, hipStream_t st) {
     // turns of a wave's 64 tasks, the last one possibly partial (has[] idles the lanes past it)
     const int turns = (a.cols / Task<TYPE>::TASK_W + WAVE - 1) / WAVE;
-    if (turns <= 1) return moe_glu_c<TYPE, 1>(a, st);
-    if (turns <= 2) return moe_glu_c<TYPE, 2>(a, st);
-    return moe_glu_c<TYPE, 4>(a, st);
+    if (turns <= 1) return moe_glu_go<TYPE, 1>(a, st);
+    if (turns <= 2) return moe_glu_go<TYPE, 2>(a, st);
+    return moe_glu_go<TYPE, 4>(a, st);
 }
 
 // ------------------------------------------------------------------------------- experts_down
