@@ -359,14 +359,15 @@ def measure_decode(torch, model, steps, device):
         out[f"p{pos + 1}"] = {"positions": pos + 1, "ms_per_token": round(ms, 4), "tok_s": round(1000.0 / ms, 1),
                               "weight_gbs": round(w_bytes / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
                               "hbm_frac": round((w_bytes + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
-    # the largest single product of a step: the Q6_K head with its fused norm + quantize
+    # the largest single product of a step: the Q6_K head (RMSNorm + quantize once, then the
+    # product: kernels.matvecs' path for launches of more than SELF_QUANTIZED_ROWS rows)
     from leat_amd import kernels
 
     x = torch.randn(1, 1, c.dim, device=device)
     norm = (model.weights.output_norm, c.norm_eps)
     head_us = _graph_us(torch, lambda: kernels.matvecs(x, model.weights.output, norm=norm), steps)
     head_bytes = model.weights.output.nbytes + c.dim * 4 + c.vocab * 4
-    out["head"] = {"kernel": "Q6_K output head 128256x4096 matvec (RMSNorm + quantize inside)", "us": round(head_us, 2),
+    out["head"] = {"kernel": "Q6_K output head 128256x4096: RMSNorm + quantize_q8, then the q8-input matvec", "us": round(head_us, 2),
                    "gbs": round(head_bytes / (head_us * 1e-6) / 1e9, 1),
                    "frac": round(head_bytes / (head_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
     return out

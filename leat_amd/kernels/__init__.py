@@ -77,6 +77,10 @@ def _q8_buffers(count: int, n: int, device: torch.device) -> Q8:
 # tokens up to which the decode kernels quantize their own f32 input (include/leatmi.h
 # leat_matvecs_f32): bit-identical to quantize_q8 followed by the product, one launch fewer
 SELF_QUANTIZED_TOKENS = 2
+# ... in launches of at most this many rows: every workgroup of such a launch normalizes and
+# quantizes x again, which past about 32768 rows (an output head: 128256) costs more than one
+# quantizer launch (130 against 94 us for a 128256 x 4096 Q6_K head on MI355X)
+SELF_QUANTIZED_ROWS = 32768
 
 
 def _self_quantized(ggml_type: GGMLType, cols: int, tokens: int) -> bool:
@@ -149,7 +153,8 @@ def matvecs(
     one_type = all(w.type == ws[0].type for w in ws) and len(ws) <= 4
     src = _f32(x)
     weight, eps = _norm_args(norm)
-    if one_type and _self_quantized(ws[0].type, cols, tokens) and _aligned16(src, weight):
+    few_rows = sum(w.shape[0] for w in ws) <= SELF_QUANTIZED_ROWS
+    if one_type and few_rows and _self_quantized(ws[0].type, cols, tokens) and _aligned16(src, weight):
         # one launch: each workgroup quantizes x itself (after the norm), then the products
         stream = _lib.stream(device)
         if residual is None:
@@ -496,7 +501,7 @@ def mixture(
 __all__ = [
     "argmax", "attention", "attention_workspace", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
     "supports_rotate",
-    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
+    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_ROWS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
     "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
     "supports_mixture", "supports_scores", "swiglu",
 ]  # fmt: skip

@@ -167,3 +167,31 @@ def test_prefill_down_bench_shape(cuda):
     sample = np.r_[0:64, 1984:2112, 4032:4096]
     want = _dense_q8(q, d, cols) @ dense[sample].T + residual[:, sample]
     assert_close(got[:, sample], want, 1e-4)
+
+
+def test_output_head_shape(cuda):
+    # config 3's Q6_K output head (128256 x 4096) with the final RMSNorm, as the decode step runs
+    # it: a launch past SELF_QUANTIZED_ROWS quantizes x once and takes the q8-input product, which
+    # must equal the one-launch f32 path bit for bit; sampled rows against the oracle
+    vocab, cols = 128256, 4096
+    rng = np.random.default_rng(77)
+    blocks = O.matrix_blocks(int(Q6_K), vocab, cols, rng, synthetic=True, scale=1e-3)
+    from leat_amd.quant import from_blocks
+
+    head = from_blocks(blocks, Q6_K, (vocab, cols))
+    x = normal(rng, 1, cols, scale=2.0)
+    weight = norm_weight(rng, cols)
+    x_gpu, w_gpu = gpu(x), gpu(weight)
+    assert vocab > kernels.SELF_QUANTIZED_ROWS
+    got = host(kernels.matvecs(x_gpu, head, norm=(w_gpu, 1e-5))[0])[0]
+    one = torch.empty(vocab, dtype=torch.float32, device=cuda)
+    _lib.call("leat_matvec_f32", int(Q6_K), head.data.data_ptr(), vocab, cols, x_gpu.data_ptr(), 1, w_gpu.data_ptr(),
+              1e-5, None, one.data_ptr(), _lib.stream())  # fmt: skip
+    np.testing.assert_array_equal(got, host(one))
+    sample = np.sort(rng.choice(vocab, 512, replace=False))
+    per_row = blocks.reshape(vocab, -1, blocks.shape[-1])[sample].reshape(-1, blocks.shape[-1])
+    dense = O.dequant(int(Q6_K), per_row, len(sample), cols).astype(np.float64)
+    xq, xd, _ = _q8_host(kernels.quantize_q8(x_gpu, (w_gpu, 1e-5)))
+    assert_close(got[sample], (_dense_q8(xq, xd, cols) @ dense.T)[0], 1e-4)
+    q, d, _ = O.quantize_q8(O.rms_norm(x, weight, 1e-5))
+    assert_close(got[sample], (_dense_q8(q, d, cols) @ dense.T)[0], 1e-3)
