@@ -231,6 +231,22 @@ int leat_rotate(const float *q, const float *k, const float *v, int tokens, int 
                 const int32_t *slots, const int32_t *positions, float *q_out, void *cache,
                 int cache_slots, int cache_positions, void *stream);
 
+/* Replaces leat/kernels/matvec.py:362-380 matvecs(x, q, k, v, norm) followed by
+ * leat/kernels/attention.py:656-782 rotate() for 1..2 tokens, in one launch: x (tokens, cols) f32
+ * RMS-normalized with norm_weight and quantized as leat_matvecs_f32 does, the q (heads * dim), k
+ * and v (kv_heads * dim rows) products, then q and k turned by RoPE over the first `rotated`
+ * dimensions of each head (pairs of adjacent dimensions, by the angles of the token's position
+ * in cos and sin), q to q_out (heads, tokens, dim) f32 and k with v stored as f16 in the cache
+ * (2, cache_slots, kv_heads, cache_positions, dim) at the token's slot and position: bit for bit
+ * what leat_matvecs_f32 then leat_rotate (halves = 0) give. dim a multiple of 16; the three
+ * matrices of one type, rows as leat_matvecs_f32 takes them. A token whose slot or position
+ * lies outside the cache stores nothing. */
+int leat_qkv_rotate_f32(int type, const void *wq, const void *wk, const void *wv, int heads,
+                        int kv_heads, int dim, int cols, const float *x, int tokens,
+                        const float *norm_weight, float eps, const float *cos, const float *sin,
+                        int rotated, const int32_t *slots, const int32_t *positions, float *q_out,
+                        void *cache, int cache_slots, int cache_positions, void *stream);
+
 /* The workspace bytes leat_attention needs for `rows` rows of `heads` heads and rows of at most
  * max_length keys. */
 int64_t leat_attention_workspace(int rows, int heads, int max_length);

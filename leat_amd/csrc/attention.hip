@@ -50,9 +50,7 @@ __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
         const int d1 = a.halves && turns ? i + half : 2 * i + 1;
         float x0 = src[d0], x1 = src[d1];
         if (turns) {
-            const float c = a.cos[(int64_t)pos * half + i], s = a.sin[(int64_t)pos * half + i];
-            const float r0 = x0 * c - x1 * s, r1 = x0 * s + x1 * c;
-            x0 = r0, x1 = r1;
+            rope_pair(x0, x1, a.cos[(int64_t)pos * half + i], a.sin[(int64_t)pos * half + i]);
         }
         if (is_q) {
             float* o = a.q_out + ((int64_t)head * a.tokens + t) * a.dim;

@@ -59,6 +59,13 @@ __device__ __forceinline__ T stream_load(const T* p) {
     return *p;
 }
 
+// RoPE of one pair of dimensions by its angle's cosine c and sine s: (x0 c - x1 s, x0 s + x1 c),
+// each as one fused multiply-add of a product, so every kernel that turns pairs rounds them alike
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, float c, float s) {
+    const float r0 = fmaf(x0, c, -(x1 * s)), r1 = fmaf(x0, s, x1 * c);
+    x0 = r0, x1 = r1;
+}
+
 // 16 bytes at a byte offset that is even but maybe not 4-aligned: 5 aligned dwords, realigned
 __device__ __forceinline__ void load16_even(const uint8_t* base, uint64_t off, uint32_t out[4]) {
     const uint32_t* p = (const uint32_t*)(base + (off & ~(uint64_t)3));

@@ -8,6 +8,19 @@ namespace leat {
 constexpr int ROWS_MATS = 4;
 constexpr int ROWS_MAX_TOKENS = 2;
 
+// The q, k and v products' rows turned by RoPE and stored for attention in the launch's epilogue
+// (leat_qkv_rotate_f32): pairs of adjacent dimensions, the first `rotated` of each head's `dim`
+struct RopeStore {
+    const float* cos;  // (cache positions, rotated / 2)
+    const float* sin;
+    int rotated, dim, kv_heads;
+    const int32_t* slots;      // tokens
+    const int32_t* positions;  // tokens
+    float* q_out;              // (heads, tokens, dim) f32; null: no epilogue
+    _Float16* cache;           // (2, cache_slots, kv_heads, cache_positions, dim)
+    int cache_slots, cache_positions;
+};
+
 struct RowsArgs {
     const uint8_t* w[ROWS_MATS];  // the GLU: gate, up
     float* out[ROWS_MATS];        // the GLU: out[0], or null when only its q8 is wanted
@@ -28,6 +41,7 @@ struct RowsArgs {
     uint32_t* hq;           // ROWS_GLU: q8 of the outputs (rows a multiple of 32), or null
     float* hd;
     float* hs;
+    RopeStore rope;         // ROWS_PLAIN over q, k, v: their RoPE and KV store (rope.q_out set)
 };
 
 // whether the row-streaming kernels take this type, row length and token count (glu: for the

@@ -149,6 +149,41 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
         }
     }
 
+    // q, k and v turned by RoPE and stored for attention (leat_qkv_rotate_f32): the workgroup's
+    // 16 rows are 8 whole pairs of adjacent dimensions of one head (dim a multiple of 16), staged
+    // in LDS and handed to a thread a (token, pair)
+    if (MODE == ROWS_PLAIN && a.rope.q_out) {
+        constexpr int TILE = WPG * RPW, PAIRS = TILE / 2;
+        static_assert(TILE % 2 == 0 && TILE <= 32, "whole pairs in the staging rows");
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int t = 0; t < B; t++)
+                if (lane == r) glu_out[t][row0 - tile_row + STEP * r] = keep[r][t];
+        __syncthreads();
+        if ((int)threadIdx.x < B * PAIRS) {
+            const RopeStore& rp = a.rope;
+            const int t = threadIdx.x / PAIRS, j = threadIdx.x % PAIRS;
+            const int pos = rp.positions[t], slot = rp.slots[t];
+            // a position or slot outside the cache stores nothing, as leat_rotate
+            if (pos >= 0 && pos < rp.cache_positions && slot >= 0 && slot < rp.cache_slots) {
+                const int rr = tile_row + 2 * j, head = rr / rp.dim, d0 = rr - head * rp.dim, i = d0 / 2;
+                const int half = rp.rotated / 2;
+                float x0 = glu_out[t][2 * j], x1 = glu_out[t][2 * j + 1];
+                if (m < 2 && i < half) rope_pair(x0, x1, rp.cos[(int64_t)pos * half + i], rp.sin[(int64_t)pos * half + i]);
+                if (m == 0) {
+                    float* o = rp.q_out + ((int64_t)head * B + t) * rp.dim + d0;
+                    o[0] = x0, o[1] = x1;
+                } else {
+                    const int64_t values = m == 2 ? (int64_t)rp.cache_slots * rp.kv_heads * rp.cache_positions * rp.dim : 0;
+                    const int64_t at = values + (((int64_t)slot * rp.kv_heads + head) * rp.cache_positions + pos) * rp.dim + d0;
+                    rp.cache[at] = (_Float16)x0;
+                    rp.cache[at + 1] = (_Float16)x1;
+                }
+            }
+        }
+    }
+
     // the GLU's own outputs quantized: the workgroup's 32 rows are one group per token
     if (MODE == ROWS_GLU && WPG * RPW == 32 && a.hq) {
 #pragma unroll
@@ -343,6 +378,38 @@ extern "C" int leat_matvecs_f32(int count, const int* types, const void* const* 
     a.count = count, a.cols = cols;
     a.x = x, a.norm = norm_weight, a.eps = eps;
     return rows_launch(types[0], ROWS_PLAIN, a, tokens, true, (hipStream_t)stream);
+}
+
+extern "C" int leat_qkv_rotate_f32(int type, const void* wq, const void* wk, const void* wv, int heads, int kv_heads,
+                                   int dim, int cols, const float* x, int tokens, const float* norm_weight, float eps,
+                                   const float* cos, const float* sin, int rotated, const int32_t* slots,
+                                   const int32_t* positions, float* q_out, void* cache, int cache_slots,
+                                   int cache_positions, void* stream) {
+    constexpr int TILE = ROWS_WPG * ROWS_RPW;
+    LEAT_REQUIRE(wq && wk && wv && slots && positions && q_out && cache, "qkv_rotate_f32: null pointer");
+    LEAT_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "qkv_rotate_f32: %d heads over %d kv heads",
+                 heads, kv_heads);
+    LEAT_REQUIRE(dim > 0 && dim % TILE == 0, "qkv_rotate_f32: heads of %d dimensions (a multiple of %d)", dim, TILE);
+    LEAT_REQUIRE(rotated >= 0 && rotated <= dim && rotated % 2 == 0, "qkv_rotate_f32: %d rotated dimensions of %d",
+                 rotated, dim);
+    LEAT_REQUIRE(rotated == 0 || (cos && sin), "qkv_rotate_f32: RoPE tables missing");
+    LEAT_REQUIRE(cache_slots > 0 && cache_positions > 0, "qkv_rotate_f32: an empty cache");
+    if (check_ptrs(type, wq, nullptr) || check_ptrs(type, wk, nullptr) || check_ptrs(type, wv, nullptr) ||
+        rows_f32_check(type, cols, x, tokens, false))
+        return -1;
+    LEAT_REQUIRE(!norm_weight || (uintptr_t)norm_weight % 16 == 0, "qkv_rotate_f32: norm weight not 16-byte aligned");
+    RowsArgs a = {};
+    const void* ws[3] = {wq, wk, wv};
+    const int rows[3] = {heads * dim, kv_heads * dim, kv_heads * dim};
+    for (int i = 0; i < 3; i++) {
+        a.w[i] = (const uint8_t*)ws[i];
+        a.out[i] = nullptr;  // the rows go to q_out and the cache only
+        a.rows[i] = rows[i];
+    }
+    a.count = 3, a.cols = cols;
+    a.x = x, a.norm = norm_weight, a.eps = eps;
+    a.rope = {cos, sin, rotated, dim, kv_heads, slots, positions, q_out, (_Float16*)cache, cache_slots, cache_positions};
+    return rows_launch(type, ROWS_PLAIN, a, tokens, true, (hipStream_t)stream);
 }
 
 extern "C" int leat_matvec_f32(int type, const void* w, int rows, int cols, const float* x, int tokens,

@@ -184,6 +184,60 @@ def matvecs(
     return [out.view(*lead, w.shape[0]) for out, w in zip(outs, ws, strict=True)]
 
 
+def supports_qkv_rotate(x: torch.Tensor, q: QTensor, k: QTensor, v: QTensor, cache: torch.Tensor, halves: bool,
+                        norm: Norm | None = None) -> bool:  # fmt: skip
+    """Whether matvecs(x, q, k, v, norm) and rotate() run as one launch (include/leatmi.h
+    leat_qkv_rotate_f32): 1..2 tokens of matrices of one type the self-quantizing kernels take,
+    adjacent-pair RoPE, an f16 cache of heads of 16k dimensions."""
+    dim, kv_heads = cache.shape[-1], cache.shape[2]
+    tokens, cols = _rows_of(x), x.shape[-1]
+    shapes = (q.shape[0] % dim == 0 and k.shape[0] == kv_heads * dim and v.shape[0] == kv_heads * dim
+              and q.shape[1] == cols == k.shape[1] == v.shape[1])  # fmt: skip
+    weight = None if norm is None else norm[0]
+    return (not halves and cache.dtype == torch.float16 and cache.is_contiguous() and dim % 16 == 0 and shapes
+            and q.type == k.type == v.type and _self_quantized(q.type, cols, tokens)
+            and (q.shape[0] + k.shape[0] + v.shape[0]) <= SELF_QUANTIZED_ROWS
+            and _aligned16(_f32(x), None if weight is None else _f32(weight)) and _on_gfx950(x))  # fmt: skip
+
+
+def qkv_rotate(
+    x: torch.Tensor, q: QTensor, k: QTensor, v: QTensor, norm: Norm | None, cache: torch.Tensor, slots, positions,
+    rope: tuple[tuple[torch.Tensor, torch.Tensor], int] | None,
+) -> torch.Tensor:  # fmt: skip
+    """matvecs(x, q, k, v, norm=norm) then rotate(q, k, v, cache, slots, positions, rope, False) in
+    one launch, bit for bit: x (1, T, cols), the f16 cache (2, slots, KV_H, positions, D) filled at
+    each token's slot and position. Returns q rotated (1, H, T, D) f32."""
+    _lib.require_device(x)
+    tokens, cols = _rows_of(x), x.shape[-1]
+    _, cache_slots, kv_heads, cache_positions, dim = cache.shape
+    heads = q.shape[0] // dim
+    device = x.device
+    src = _f32(x).contiguous()
+    weight, eps = _norm_args(norm)
+    out = torch.empty(heads * tokens * dim, dtype=torch.float32, device=device)
+    slot_rows = _device_rows(slots, device)
+    pos_rows = _device_rows(positions, device)
+    if rope is None:
+        cos = sin = None
+        rotated = 0
+    else:
+        (cos, sin), rotated = (t.float().contiguous() for t in rope[0]), rope[1]
+        if cos.shape[0] < cache_positions:
+            raise _lib.LeatError("qkv_rotate: the RoPE tables must cover every position of the cache")
+    _lib.call("leat_qkv_rotate_f32", int(q.type), _blocks(q), _blocks(k), _blocks(v), heads, kv_heads, dim, cols,
+              src.data_ptr(), tokens, _lib.ptr(weight), eps, _lib.ptr(cos), _lib.ptr(sin), rotated,
+              slot_rows.data_ptr(), pos_rows.data_ptr(), out.data_ptr(), cache.data_ptr(), cache_slots,
+              cache_positions, _lib.stream(device))  # fmt: skip
+    return out.view(1, heads, tokens, dim)
+
+
+def _device_rows(values, device: torch.device) -> torch.Tensor:
+    # an int32 device tensor of per-token slots or positions (a tensor as given, or a list)
+    if isinstance(values, torch.Tensor):
+        return values.to(device=device, dtype=torch.int32).contiguous()
+    return torch.tensor(list(values), dtype=torch.int32, device=device)
+
+
 def swiglu(
     x: torch.Tensor, gate: QTensor, up: QTensor, norm: Norm | None = None, kind: str = "silu"
 ) -> torch.Tensor:
@@ -501,7 +555,7 @@ def mixture(
 __all__ = [
     "argmax", "attention", "attention_workspace", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
     "supports_rotate",
-    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_ROWS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls",
+    "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_ROWS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls", "qkv_rotate", "supports_qkv_rotate",
     "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
     "supports_mixture", "supports_scores", "swiglu",
 ]  # fmt: skip

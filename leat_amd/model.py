@@ -233,9 +233,8 @@ class Model:
         scale = 1.0 / math.sqrt(c.head_dim)
         rope = (self.rope, c.head_dim)
         for layer, cache in zip(w.layers, self.cache, strict=True):
-            q, k, v = ops.linears(x, layer.q, layer.k, layer.v, norm=(layer.attn_norm, c.norm_eps))
-            q_rot, _ = ops.rotate(q.view(1, B, c.heads, c.head_dim), k.view(1, B, c.kv_heads, c.head_dim),
-                                  v.view(1, B, c.kv_heads, c.head_dim), cache, None, rope, False, slots, positions)  # fmt: skip
+            q_rot = ops.qkv_rotate(x, layer.q, layer.k, layer.v, (layer.attn_norm, c.norm_eps), cache, None, rope, False,
+                                   slots, positions)  # fmt: skip
             att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context, self._attention_workspace(B))
             x = ops.linear(att, layer.o, residual=x)
             x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))

@@ -265,6 +265,27 @@ def rotate(
     return torch.cat(outs, dim=2), cache
 
 
+def qkv_rotate(
+    x: torch.Tensor, wq: QTensor, wk: QTensor, wv: QTensor, norm: tuple[torch.Tensor, float] | None,
+    cache: torch.Tensor, spans: list[Span] | None, rope: tuple[tuple[torch.Tensor, torch.Tensor], int] | None,
+    halves: bool, slots=None, positions=None,
+) -> torch.Tensor:  # fmt: skip
+    """An attention layer's inputs: linears(x, wq, wk, wv, norm=norm) then rotate() of the three
+    into the cache (leat/model.py:397-401: the q, k, v products, RoPE and the KV store), in one
+    launch where the kernels take the shapes, with the same results. Returns q rotated (1, H, T, D)
+    f32."""
+    if slots is None:
+        slots, positions = _span_rows(spans)
+    if not reference_mode() and kernels.supports_qkv_rotate(x, wq, wk, wv, cache, halves, norm):
+        return kernels.qkv_rotate(x, wq, wk, wv, norm, cache, slots, positions, rope)
+    dim, kv_heads = cache.shape[-1], cache.shape[2]
+    T = x.shape[-2]
+    q, k, v = linears(x, wq, wk, wv, norm=norm)
+    q_rot, _ = rotate(q.reshape(1, T, wq.shape[0] // dim, dim), k.reshape(1, T, kv_heads, dim),
+                      v.reshape(1, T, kv_heads, dim), cache, None, rope, halves, slots, positions)  # fmt: skip
+    return q_rot
+
+
 def attention(
     q: torch.Tensor, cache: torch.Tensor, spans: list[Span] | None, scale: float, slots=None, lengths=None,
     max_length: int | None = None, workspace: torch.Tensor | None = None,

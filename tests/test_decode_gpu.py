@@ -71,6 +71,37 @@ def test_rotate(cuda, halves, rotated):
     np.testing.assert_allclose(host(ref_cache).astype(np.float32), stored.astype(np.float32), rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("rotated", [128, 64])
+@pytest.mark.parametrize("rows", [[(1, 37)], [(0, 5), (2, 511)], [(1, 600)]])
+def test_qkv_rotate_fused(cuda, rows, rotated):
+    # the q, k, v products with RoPE and the KV store in one launch (leat_qkv_rotate_f32) against
+    # linears() then rotate(): q and the whole cache bit for bit, at Llama-3-8B's attention shapes
+    # (32 heads, 8 kv heads of 128, 4096 columns of Q4_K); a position past the cache (600 of 512)
+    # stores nothing in either
+    rng = np.random.default_rng(len(rows) + rotated)
+    heads, kv_heads, dim, cols, positions = 32, 8, 128, 4096, 512
+    wq, wk, wv = (make_weights(GGMLType.Q4_K, n * dim, cols, rng, synthetic=True).q for n in (heads, kv_heads, kv_heads))
+    x = gpu(normal(rng, 1, len(rows), cols, scale=2.0))
+    norm = (gpu(rng.uniform(0.5, 1.5, cols).astype(np.float32)), 1e-5)
+    angles = rng.uniform(0, 6, (positions, rotated // 2)).astype(np.float32)
+    rope = ((gpu(np.cos(angles)), gpu(np.sin(angles))), rotated)
+    spans = [ops.Span(s, p) for s, p in rows]
+    fused = torch.zeros(2, SLOTS, kv_heads, positions, dim, dtype=torch.float16, device=cuda)
+    split = torch.zeros_like(fused)
+    assert kernels.supports_qkv_rotate(x, wq, wk, wv, fused, False, norm)
+    got = host(ops.qkv_rotate(x, wq, wk, wv, norm, fused, spans, rope, False))
+    q, k, v = ops.linears(x, wq, wk, wv, norm=norm)
+    T = len(rows)
+    want, _ = ops.rotate(q.reshape(1, T, heads, dim), k.reshape(1, T, kv_heads, dim), v.reshape(1, T, kv_heads, dim),
+                         split, spans, rope, False)  # fmt: skip
+    want = host(want)
+    for t, (_, pos) in enumerate(rows):
+        if pos < positions:
+            np.testing.assert_array_equal(got[:, :, t], want[:, :, t])
+    np.testing.assert_array_equal(host(fused).view(np.uint16), host(split).view(np.uint16))
+    assert host(fused).any() == any(pos < positions for _, pos in rows)
+
+
 # cache positions and lengths of leat's test_attention (tests/test_kernels.py:493-511)
 @pytest.mark.parametrize("n, length", [(64, 1), (64, 64), (1024, 63), (1024, 65), (1024, 1000), (3072, 3072),
                                        (4096, 3079), (4096, 4096), (16384, 9000)])  # fmt: skip
