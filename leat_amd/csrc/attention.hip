@@ -67,8 +67,8 @@ __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
 
 // --------------------------------------------------------------------------------- attention
 
-constexpr int ATT_WAVES = 4;                       // waves a workgroup
-constexpr int ATT_WAVE_KEYS = 32;                  // keys a wave takes per round
+constexpr int ATT_WAVES = 8;                       // waves a workgroup
+constexpr int ATT_WAVE_KEYS = 16;                  // keys a wave takes per round
 constexpr int ATT_KEYS = ATT_WAVES * ATT_WAVE_KEYS;  // keys a workgroup takes per round
 constexpr int ATT_CHUNKS = 64;                     // most workgroups per (row, kv head): longer rows loop
 constexpr int ATT_DIM = 128;                       // head dimension: a pair of dimensions a lane
@@ -149,13 +149,13 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
     for (int h = 0; h < G; h++) m[h] = NEG, l[h] = 0.0f, acc[h][0] = acc[h][1] = 0.0f;
 
     for (int base = chunk * ATT_KEYS + w * ATT_WAVE_KEYS; base < length; base += a.chunks * ATT_KEYS) {
-        // the round's keys and values are all read at once (64 reads in flight a wave)
+        // the round's keys and values are all read at once (2 ATT_WAVE_KEYS reads in flight a wave)
         uint32_t kv[ATT_WAVE_KEYS], vv[ATT_WAVE_KEYS];
 #pragma unroll
         for (int j = 0; j < ATT_WAVE_KEYS; j++) kv[j] = keys[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
 #pragma unroll
         for (int j = 0; j < ATT_WAVE_KEYS; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
-        // scores of keys base .. base + 31: 16 keys at a time, lane l's share of each dot product
+        // scores of keys base .. base + ATT_WAVE_KEYS - 1: 16 keys at a time, lane l's share of each dot product
 #pragma unroll
         for (int sb = 0; sb < ATT_WAVE_KEYS / 16; sb++) {
 #pragma unroll
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
                 if ((lane & 3) == 0) scores[w][h][16 * sb + (lane >> 2)] = s;
             }
         }
-        // the online softmax, a key a lane (lanes 32.. idle): rescale by the new maximum's step
+        // the online softmax, a key a lane (lanes ATT_WAVE_KEYS.. idle): rescale by the new maximum's step
         const int keys_here = min(ATT_WAVE_KEYS, length - base);
         const bool valid = lane < keys_here;
 #pragma unroll
