@@ -208,7 +208,7 @@ def measure(torch, lib, layers, B, steps, warmup, device):
     weight_bytes = LAYERS * LAYER_BYTES
     gbs = weight_bytes / (ms * 1e-3) / 1e9
     achieved = glu_bytes(B) / (glu_us * 1e-6) / 1e9
-    traffic, note = profiled_traffic(GLU_KERNELS.get(B, ""))
+    traffic, note = profiled_traffic(f"decode_glu_b{B}")
     return {
         "ms_per_step": ms,
         "weight_gbs": gbs,
@@ -223,10 +223,10 @@ def measure(torch, lib, layers, B, steps, warmup, device):
     }
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "decode_linear_hbm_bytes.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_moe_hbm_bytes.md"
 # the sources of the decode kernels whose HBM bytes that profile records
 TRAFFIC_SOURCES = ["blocks.h", "common.h", "q8.h", "rows.h", "rows.hip", "rowtask.h", "tiles.h", "tiles.hip",
-                   "mmv.h", "mmv.hip", "matvec.hip"]  # fmt: skip
+                   "mmv.h", "mmv.hip", "matvec.hip", "experts.hip", "attention.hip"]  # fmt: skip
 
 
 # the prefill kernels' sources, whose counters profiles/prefill_counters.md records
@@ -263,10 +263,12 @@ def profiled_counters(kernel: str) -> dict | None:
     return {**{k: float(v) for k, v in fields.items()}, "source": f"profiles/{COUNTER_PROFILE.name}, sources sha {sha}"}
 
 
-def profiled_traffic(kernel: str) -> tuple[int | None, str]:
-    """HBM bytes per dispatch of `kernel` as the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    records them (calibrated against a copy of known size), and where that figure comes from; None
-    where the summary has no line for it, or was measured on other kernel sources than these."""
+def profiled_traffic(label: str) -> tuple[int | None, str]:
+    """HBM bytes per dispatch of a roofline kernel (`label`: decode_glu_b1, moe_glu_b8,
+    attention_p4096, ...) as the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary records them
+    ("traffic <label> <bytes>", calibrated against a copy of known size), and where that figure
+    comes from; None where the summary has no line for it, or was measured on other kernel
+    sources than these."""
     try:
         text = TRAFFIC_PROFILE.read_text()
     except OSError:
@@ -274,7 +276,7 @@ def profiled_traffic(kernel: str) -> tuple[int | None, str]:
     m = re.search(r"^sources sha ([0-9a-f]+)$", text, re.M)
     if not m or m.group(1) != sources_sha():
         return None, f"{TRAFFIC_PROFILE.name} was measured on other kernel sources (sha {m.group(1) if m else '?'})"
-    m = re.search(r"^" + re.escape(kernel) + r" (\d+)$", text, re.M)
+    m = re.search(r"^traffic " + re.escape(label) + r" (\d+)$", text, re.M)
     if not m:
         return None, f"{TRAFFIC_PROFILE.name} has no line for this kernel"
     return int(m.group(1)), f"profiles/{TRAFFIC_PROFILE.name}: rocprofv3 FETCH_SIZE + WRITE_SIZE, sources sha {sources_sha()}"
@@ -297,9 +299,6 @@ def _graph_us(torch, fn, reps, inner=1):
     torch.cuda.synchronize()
     return 1000 * start.elapsed_time(end) / (reps * inner)
 
-
-# the GLU kernels of the decode legs, as rocprofv3 names them
-GLU_KERNELS = {1: "rows_kernel<12, 1, 2, 4, 8, 2, true, true>", 4: "tiles_kernel<12, 2, 4>", 8: "tiles_kernel<12, 2, 4>"}
 
 def decode_model(torch, layers, seed, device):
     """Config 3's model around the config-2 layers' weights (shared, not copied): a Q4_K token
@@ -328,12 +327,13 @@ def decode_model(torch, layers, seed, device):
     return model
 
 
-def measure_decode(torch, model, steps, device):
+def measure_decode(torch, model, steps, device, positions=(1, 4096)):
     """Config 3: the full single-stream decode step (embedding, 32 layers with RoPE + KV store and
-    FlashDecoding over the cache, final norm + Q6_K head, argmax) as one HIP-graph replay, at 1
-    and at 4095 cached positions (the step's token at position 0, then at 4095 of a 4096-position
-    cache). tok/s is one token per step; GB/s counts the matrices streamed (layers and head, as
-    leat's bench does) and, for hbm_frac, the keys and values read too."""
+    FlashDecoding over the cache, final norm + Q6_K head, argmax) as one HIP-graph replay, at each
+    of `positions` cached positions (by default 1 and 4096: the step's token at position 0, then
+    at 4095 of a 4096-position cache). tok/s is one token per step; GB/s counts the matrices
+    streamed (layers and head, as leat's bench does) and, for hbm_frac, the keys and values read
+    too. FlashDecoding alone over the 32 layers' caches gets a roofline line of its own."""
     from leat_amd.model import GraphStep, weight_bytes
 
     c = model.config
@@ -341,7 +341,7 @@ def measure_decode(torch, model, steps, device):
     w_bytes = weight_bytes(model.weights)
     out = {"workload": "llama3.1-8b q4_k_m random-init decode step, B=1 (embedding .. argmax)",
            "weight_bytes_per_token": w_bytes}  # fmt: skip
-    for pos in (0, c.context - 1):
+    for pos in (p - 1 for p in positions):
         step.positions.fill_(pos)
         step.tokens.fill_(128000)
         torch.cuda.synchronize()
@@ -359,6 +359,24 @@ def measure_decode(torch, model, steps, device):
         out[f"p{pos + 1}"] = {"positions": pos + 1, "ms_per_token": round(ms, 4), "tok_s": round(1000.0 / ms, 1),
                               "weight_gbs": round(w_bytes / (ms * 1e-3) / 1e9, 1), "kv_bytes": kv,
                               "hbm_frac": round((w_bytes + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
+    # FlashDecoding alone (partial sums and their combine) over every layer's cache at the last
+    # positions: the keys and values of (pos + 1) positions a layer, read once
+    from leat_amd import ops
+
+    pos = positions[-1] - 1
+    q = torch.randn(1, c.heads, 1, c.head_dim, device=device)
+    slots = torch.zeros(1, dtype=torch.int32, device=device)
+    lengths = torch.full((1,), pos + 1, dtype=torch.int32, device=device)
+    work = model._attention_workspace(1)
+    att_us = _graph_us(torch, lambda: [ops.attention(q, cache, None, c.head_dim**-0.5, slots, lengths, c.context, work)
+                                       for cache in model.cache], steps) / c.layers  # fmt: skip
+    att_bytes = (pos + 1) * 2 * c.kv_heads * c.head_dim * 2 + c.heads * c.head_dim * 4 * 2
+    att_gbs = att_bytes / (att_us * 1e-6) / 1e9
+    att_traffic, att_note = profiled_traffic(f"attention_p{pos + 1}")
+    out["attention"] = {"kernel": f"FlashDecoding over {pos + 1} positions, 32 heads over 8 kv heads of 128 (partial + combine)",
+                        "us": round(att_us, 2), "bytes_per_launch": att_bytes,
+                        "roofline": {"bound": "hbm", "achieved": att_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                     "frac": att_gbs / HBM_PEAK_GBS, "traffic": att_traffic, "traffic_source": att_note}}  # fmt: skip
     # the largest single product of a step: the Q6_K head (RMSNorm + quantize once, then the
     # product: kernels.matvecs' path for launches of more than SELF_QUANTIZED_ROWS rows)
     from leat_amd import kernels
@@ -527,13 +545,14 @@ def measure_moe(torch, lib, B, steps, device, layers):
                  + P * (MOE_HIDDEN + MOE_HIDDEN // 32 * 8))  # fmt: skip
     gbs = step_bytes / (step_us * 1e-6) / 1e9
     glu_gbs = glu_bytes / (glu_us * 1e-6) / 1e9
+    moe_traffic, moe_note = profiled_traffic(f"moe_glu_b{B}")
     return {
         "batch": B, "layers": MOE_LAYERS, "distinct_experts_per_layer": round(sum(distinct) / len(distinct), 2),
         "us_per_layer": round(step_us / MOE_LAYERS, 2), "weight_gbs": round(gbs, 1),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "tok_s": round(B * 1e6 / step_us, 1),
         "glu_us": round(glu_us, 2), "down_us": round(down_us, 2),
         "roofline": {"bound": "hbm", "achieved": glu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": glu_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "frac": glu_gbs / HBM_PEAK_GBS, "traffic": moe_traffic, "traffic_source": moe_note,
                      "kernel": f"expert gate+up GLU matvec, {last} of 128 experts 2x768x2048 Q4_K, B={B}",
                      "bytes_per_launch": glu_bytes},
     }  # fmt: skip
@@ -623,6 +642,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs", default="batches,decode,prefill,moe",
                     help="configurations beside the headline: batches (B=4, 8, 16), decode, prefill, moe")  # fmt: skip
+    ap.add_argument("--batches", default="4,8,16", help="the batch sizes of the batches leg")
+    ap.add_argument("--moe-batches", default="1,8", help="the batch sizes of the moe leg")
+    ap.add_argument("--positions", default="1,4096", help="the cached positions of the decode leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 256 MiB device to device: the calibration kernel of HBM byte counters")  # fmt: skip
     args = ap.parse_args()
@@ -648,16 +670,17 @@ def main():
     print(f"B=1: {b1['ms_per_step']:.3f} ms/step, {b1['weight_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     batches = {}
     if "batches" in args.legs:
-        for B in (4, 8, 16):
+        for B in (int(b) for b in args.batches.split(",") if b):
             batches[f"b{B}"] = _leg(measure(torch, lib, layers, B, args.steps, args.warmup, device))
             print(f"B={B}: {batches[f'b{B}']['ms_per_step']:.3f} ms/step, {batches[f'b{B}']['weight_gbs']:.0f} GB/s",
                   file=sys.stderr, flush=True)  # fmt: skip
     decode = prefill = moe = None
     if "decode" in args.legs:
         model = decode_model(torch, layers, args.seed, device)
-        decode = measure_decode(torch, model, max(10, args.steps // 2), device)
-        print(f"decode: P=1 {decode['p1']['tok_s']:.0f} tok/s, P=4096 {decode['p4096']['tok_s']:.0f} tok/s",
-              file=sys.stderr, flush=True)  # fmt: skip
+        positions = tuple(int(p) for p in args.positions.split(",") if p)
+        decode = measure_decode(torch, model, max(10, args.steps // 2), device, positions)
+        print("decode: " + ", ".join(f"P={p} {decode[f'p{p}']['tok_s']:.0f} tok/s" for p in positions)
+              + f"; attention {decode['attention']['us']:.1f} us", file=sys.stderr, flush=True)  # fmt: skip
         del model
     if "prefill" in args.legs:
         prefill = measure_prefill(torch, lib, layers[0], max(5, args.steps // 5), device)
@@ -667,8 +690,9 @@ def main():
     torch.cuda.empty_cache()
     if "moe" in args.legs:
         experts = moe_layers(torch, device, args.seed)
-        moe = {f"b{B}": measure_moe(torch, lib, B, max(5, args.steps // 5), device, experts) for B in (1, 8)}
-        print(f"moe: B=1 {moe['b1']['us_per_layer']:.1f} us/layer, B=8 {moe['b8']['us_per_layer']:.1f} us/layer",
+        moe = {f"b{B}": measure_moe(torch, lib, B, max(5, args.steps // 5), device, experts)
+               for B in (int(b) for b in args.moe_batches.split(",") if b)}  # fmt: skip
+        print("moe: " + ", ".join(f"{k} {v['us_per_layer']:.1f} us/layer" for k, v in moe.items()),
               file=sys.stderr, flush=True)  # fmt: skip
         del experts
     if args.copy_probe:
