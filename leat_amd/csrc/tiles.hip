@@ -4,8 +4,10 @@
 // kernels of mmv.hip instead.
 //
 // Work split: a workgroup owns a tile of 32 consecutive rows (of gate and of up for the GLU); its
-// S waves split the rows' blocks between them, each streaming a contiguous run of blocks, and add
-// their sums through LDS at the end.
+// S waves take every S-th block of the rows (wave w blocks w, w + S, ...), so at each step they
+// read neighbouring blocks, whose shared 128-byte lines (a block is 144 bytes) are fetched once
+// (contiguous runs a wave fetched 20% more than the weights); they add their sums through LDS at
+// the end.
 //
 // Memory: every lane loads exactly the bytes its MFMA operand needs (row r = lane % 32, half
 // h = lane / 32 of each group of 32 weights) straight into registers, the next block's loads in
@@ -150,12 +152,11 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
     wr[0] = (MODE == TILES_GLU ? a.w[0] : a.w[m]) + (size_t)row * row_bytes;
     if (NM == 2) wr[NM - 1] = a.w[1] + (size_t)row * row_bytes;
 
-    // the wave's blocks, and the first one's loads before anything else
-    const int b0 = nb * w / S, b1 = nb * (w + 1) / S;
+    // the wave's blocks w, w + S, ..., and the first one's loads before anything else
     typename TB::Raw cur[NM];
-    if (b0 < b1)
+    if (w < nb)
 #pragma unroll
-        for (int k = 0; k < NM; k++) cur[k] = TB::load(wr[k], b0, h);
+        for (int k = 0; k < NM; k++) cur[k] = TB::load(wr[k], w, h);
 
     // the tokens' scale tables into LDS, group-major: read in the source's order (token-major)
     TileActs x;
@@ -180,15 +181,15 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; v++) acc[k][v] = 0.0f;
 
-    for (int b = b0; b < b1; b++) {
+    for (int b = w; b < nb; b += S) {
         v4i xa[8];
         x.operands(b, xa);
         typename TB::Raw nxt[NM];
-        if (b + 1 < b1)
+        if (b + S < nb)
 #pragma unroll
-            for (int k = 0; k < NM; k++) nxt[k] = TB::load(wr[k], b + 1, h);
+            for (int k = 0; k < NM; k++) nxt[k] = TB::load(wr[k], b + S, h);
         TileCompute<TYPE>::template run<NM>(cur, b, xa, x, h, acc);
-        if (b + 1 < b1)
+        if (b + S < nb)
 #pragma unroll
             for (int k = 0; k < NM; k++) cur[k] = nxt[k];
     }
