@@ -220,7 +220,7 @@ static int dispatch(int type, MatvecArgs& a, int tokens, hipStream_t s) {
         r.hq = a.hq, r.hd = a.hd, r.hs = a.hs;
         return rows_launch(type, MODE, r, tokens, false, s);
     }
-    // 3..8 tokens: the GLU on the tile kernels; the plain and residual products (where they fit)
+    // 3..16 tokens: the GLU on the tile kernels; the plain and residual products (where they fit)
     // on the staged ones, which measured faster for them
     if (tiles_fits(type, a.cols, tokens, (const void* const*)a.w, nw) &&
         (MODE == MODE_GLU || !mmv_fits(type, a.cols, tokens, (const void* const*)a.w, nw))) {

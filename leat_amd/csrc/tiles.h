@@ -1,4 +1,4 @@
-// The matrix-core decode kernels for 3..8 tokens (tiles.hip), shared with matvec.hip.
+// The matrix-core decode kernels for 3..16 tokens of Q4_K (tiles.hip), shared with matvec.hip.
 #pragma once
 
 #include "common.h"

@@ -1,4 +1,4 @@
-// Decode products for 3..8 tokens of Q4_K weights on matrix cores: y[t, row] = W[row] . x[t],
+// Decode products for 3..16 tokens of Q4_K weights on matrix cores: y[t, row] = W[row] . x[t],
 // every weight read once for all tokens (leat/kernels/matvec.py:1-4, 306-395 at batch sizes above
 // two). Q6_K's 210-byte blocks, which do not split into aligned 16-byte runs, take the LDS-staged
 // kernels of mmv.hip instead.
@@ -17,7 +17,8 @@
 // Math: v_mfma_i32_32x32x32_i8 with the rows as N (operand B: lane l holds row l % 32) and the
 // tokens as M (operand A: lane l holds token l % 32, zero past the last), K one group of 32. The
 // int32 result in lane l is row l % 32 for tokens 8(v / 4) + 4h + v % 4 of its registers v; with
-// at most 8 tokens the useful ones are v = 0..3, tokens 4h + v, scaled into f32 per group as
+// at most 8 tokens (TOK = 8) the useful ones are v = 0..3, tokens 4h + v, with at most 16 v = 0..7,
+// and they are scaled into f32 per group as
 // leat's kernels combine each group's int32 dot (leat/kernels/matvec.py:107-181): lane h takes
 // qs bytes [32j + 16h, +16) of pair j, whose low nibbles are group 2j's values 16h..16h+15 and
 // high nibbles group 2j+1's; acc += d*sc*xd*D - dmin*m*xs.
@@ -63,8 +64,8 @@ struct TileBlock<Q4_K> {
 };
 
 // The tokens' activations: the q8 words of token t, group g at word t * cols / 4 + 8 g in global
-// memory; the scale tables in LDS, group-major, 8 token slots a group (zero past the last token),
-// d then s.
+// memory; the scale tables in LDS, group-major, TOK token slots a group (zero past the last
+// token), d then s.
 struct TileActs {
     const uint32_t* words;  // the lane's (token, half) words: token * cols / 4 + 4 h
     bool live;              // the lane's token is one of the tokens
@@ -81,21 +82,22 @@ struct TileActs {
             xa[s] = live ? v : zero;
         }
     }
-    __device__ float4 scales(int off, int g, int h) const {
-        return *(const float4*)((const float*)tiles_lds + off + 8 * g + 4 * h);
+    // tokens 8q + 4h .. 8q + 4h + 3 of group g, in a table of `tok` slots a group
+    __device__ float4 scales(int off, int tok, int g, int q, int h) const {
+        return *(const float4*)((const float*)tiles_lds + off + tok * g + 8 * q + 4 * h);
     }
 };
 
 // One block of NM matrices (gate and up for the GLU) for the lane: acc[k][v] += matrix k's share
-// for the tokens 4h + v. Each group's operand A and scale tables are read once for the matrices,
-// whose products are issued back to back.
+// for the tokens 8(v / 4) + 4h + v % 4, v < TOK / 2. Each group's operand A and scale tables are
+// read once for the matrices, whose products are issued back to back.
 template <int TYPE> struct TileCompute;
 
 template <>
 struct TileCompute<Q4_K> {
-    template <int NM>
+    template <int NM, int TOK>
     __device__ static void run(const TileBlock<Q4_K>::Raw (&raw)[NM], int b, const v4i (&xa)[8], const TileActs& x,
-                               int h, float (&acc)[NM][4]) {
+                               int h, float (&acc)[NM][TOK / 2]) {
         float d[NM], dmin[NM];
 #pragma unroll
         for (int k = 0; k < NM; k++) d[k] = f16_lo(raw[k].hdr[0]), dmin[k] = f16_hi(raw[k].hdr[0]);
@@ -105,7 +107,9 @@ struct TileCompute<Q4_K> {
             for (int e = 0; e < 2; e++) {
                 const int s = 2 * j + e, g = 8 * b + s;
                 const v4i a = xa[s];
-                const float4 xd = x.scales(x.d_off, g, h), xs = x.scales(x.s_off, g, h);
+                float4 xd[TOK / 8], xs[TOK / 8];
+#pragma unroll
+                for (int q = 0; q < TOK / 8; q++) xd[q] = x.scales(x.d_off, TOK, g, q, h), xs[q] = x.scales(x.s_off, TOK, g, q, h);
                 v16i D[NM];
 #pragma unroll
                 for (int k = 0; k < NM; k++) {
@@ -120,20 +124,24 @@ struct TileCompute<Q4_K> {
                     const uint32_t scv = s < 4 ? (x0 & 63u) : ((x2 & 15u) | ((x0 >> 2) & 0x30u));
                     const uint32_t mv = s < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
                     const float sc = d[k] * (float)scv, mn = dmin[k] * (float)mv;
-                    acc[k][0] += sc * xd.x * (float)D[k][0] - mn * xs.x;
-                    acc[k][1] += sc * xd.y * (float)D[k][1] - mn * xs.y;
-                    acc[k][2] += sc * xd.z * (float)D[k][2] - mn * xs.z;
-                    acc[k][3] += sc * xd.w * (float)D[k][3] - mn * xs.w;
+#pragma unroll
+                    for (int q = 0; q < TOK / 8; q++) {
+                        acc[k][4 * q + 0] += sc * xd[q].x * (float)D[k][4 * q + 0] - mn * xs[q].x;
+                        acc[k][4 * q + 1] += sc * xd[q].y * (float)D[k][4 * q + 1] - mn * xs[q].y;
+                        acc[k][4 * q + 2] += sc * xd[q].z * (float)D[k][4 * q + 2] - mn * xs[q].z;
+                        acc[k][4 * q + 3] += sc * xd[q].w * (float)D[k][4 * q + 3] - mn * xs[q].w;
+                    }
                 }
             }
         }
     }
 };
 
-template <int TYPE, int MODE, int S>
+template <int TYPE, int MODE, int S, int TOK>
 __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
     using TB = TileBlock<TYPE>;
     constexpr int NM = MODE == TILES_GLU ? 2 : 1;
+    constexpr int TV = TOK / 2;  // result registers a lane keeps: tokens 8(v / 4) + 4h + v % 4
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int r = lane & 31, h = lane >> 5;
@@ -161,25 +169,25 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
     // the tokens' scale tables into LDS, group-major: read in the source's order (token-major)
     TileActs x;
     x.d_off = 0;
-    x.s_off = 8 * G;
+    x.s_off = TOK * G;
     {
         float* tab = (float*)tiles_lds;
-        for (int i = threadIdx.x; i < 8 * G; i += S * 64) {
+        for (int i = threadIdx.x; i < TOK * G; i += S * 64) {
             const int t = i / G, g = i - t * G;
             const bool in = t < tokens;
-            tab[8 * g + t] = in ? a.xd[i] : 0.0f;
-            tab[8 * G + 8 * g + t] = in ? a.xs[i] : 0.0f;
+            tab[TOK * g + t] = in ? a.xd[i] : 0.0f;
+            tab[TOK * G + TOK * g + t] = in ? a.xs[i] : 0.0f;
         }
         __syncthreads();
     }
     x.live = r < tokens;
     x.words = (const uint32_t*)a.xq + (int64_t)(x.live ? r : 0) * (cols / 4) + 4 * h;
 
-    float acc[NM][4];
+    float acc[NM][TV];
 #pragma unroll
     for (int k = 0; k < NM; k++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) acc[k][v] = 0.0f;
+        for (int v = 0; v < TV; v++) acc[k][v] = 0.0f;
 
     for (int b = w; b < nb; b += S) {
         v4i xa[8];
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
         if (b + S < nb)
 #pragma unroll
             for (int k = 0; k < NM; k++) nxt[k] = TB::load(wr[k], b + S, h);
-        TileCompute<TYPE>::template run<NM>(cur, b, xa, x, h, acc);
+        TileCompute<TYPE>::template run<NM, TOK>(cur, b, xa, x, h, acc);
         if (b + S < nb)
 #pragma unroll
             for (int k = 0; k < NM; k++) cur[k] = nxt[k];
@@ -201,24 +209,24 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
 #pragma unroll
         for (int k = 0; k < NM; k++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) red[((w * NM + k) * 4 + v) * 64 + lane] = acc[k][v];
+            for (int v = 0; v < TV; v++) red[((w * NM + k) * TV + v) * 64 + lane] = acc[k][v];
         __syncthreads();
         if (w != 0) return;
 #pragma unroll
         for (int k = 0; k < NM; k++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
+            for (int v = 0; v < TV; v++) {
                 float sum = 0.0f;
-                for (int i = 0; i < S; i++) sum += red[((i * NM + k) * 4 + v) * 64 + lane];
+                for (int i = 0; i < S; i++) sum += red[((i * NM + k) * TV + v) * 64 + lane];
                 acc[k][v] = sum;
             }
     }
-    // wave 0: lane (r, h) holds row row0 + r for tokens 4h + v
+    // wave 0: lane (r, h) holds row row0 + r for tokens 8(v / 4) + 4h + v % 4
     const bool row_in = row0 + r < rows;
-    float y[4];
+    float y[TV];
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int t = 4 * h + v;
+    for (int v = 0; v < TV; v++) {
+        const int t = 8 * (v / 4) + 4 * h + v % 4;
         y[v] = acc[0][v];
         if (MODE == TILES_GLU) y[v] = glu(a.kind, acc[0][v], acc[NM - 1][v]);
         const int64_t at = (int64_t)t * rows + row0 + r;
@@ -229,8 +237,8 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
     // the GLU's outputs quantized: for each token the tile's 32 rows are one group of 32
     if (MODE == TILES_GLU && a.hq) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int t = 4 * h + v;
+        for (int v = 0; v < TV; v++) {
+            const int t = 8 * (v / 4) + 4 * h + v % 4;
             float amax = fabsf(y[v]);
 #pragma unroll
             for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
@@ -260,45 +268,51 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
 
 constexpr int TILES_WAVES = 2048;  // waves a launch aims for
 
-template <int TYPE, int MODE, int S>
+template <int TYPE, int MODE, int S, int TOK>
 static int tiles_go(TileArgs& a, hipStream_t st) {
     const int tiles = a.tile_start[a.count];
     const int G = a.cols / GROUP;
-    const size_t acts = (size_t)2 * 8 * G * 4;  // the scale tables
-    const size_t red = (size_t)S * (MODE == TILES_GLU ? 2 : 1) * 4 * 64 * 4;
+    const size_t acts = (size_t)2 * TOK * G * 4;  // the scale tables
+    const size_t red = (size_t)S * (MODE == TILES_GLU ? 2 : 1) * (TOK / 2) * 64 * 4;
     const size_t lds = acts > red ? acts : red;
     // a workgroup's LDS beyond 64 KB is allowed once per kernel
-    static const hipError_t allowed = hipFuncSetAttribute((const void*)tiles_kernel<TYPE, MODE, S>,
+    static const hipError_t allowed = hipFuncSetAttribute((const void*)tiles_kernel<TYPE, MODE, S, TOK>,
                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
                                                           (int)TILES_MAX_LDS);
     if (allowed != hipSuccess && lds > 64 * 1024) {
         set_error("tiles: %zu bytes of LDS refused", lds);
         return -1;
     }
-    hipLaunchKernelGGL((tiles_kernel<TYPE, MODE, S>), dim3(tiles), dim3(S * 64), lds, st, a);
+    hipLaunchKernelGGL((tiles_kernel<TYPE, MODE, S, TOK>), dim3(tiles), dim3(S * 64), lds, st, a);
     return check_launch("tiles");
 }
 
-template <int TYPE, int MODE>
+template <int TYPE, int MODE, int TOK>
 static int tiles_s(TileArgs& a, hipStream_t st) {
     const int tiles = a.tile_start[a.count];
     const int blocks = a.cols / 256;
     // waves per tile: enough for the launch to fill the GPU, a few blocks each
     const int want = (TILES_WAVES + tiles - 1) / tiles;
-    // (16 waves fit 1024 threads' 128 registers a lane only for the plain products)
-    if constexpr (MODE != TILES_GLU)
-        if (want >= 16 && blocks >= 32) return tiles_go<TYPE, MODE, 16>(a, st);
-    if (want >= 8 && blocks >= 16) return tiles_go<TYPE, MODE, 8>(a, st);
-    if (want >= 4 && blocks >= 8) return tiles_go<TYPE, MODE, 4>(a, st);
-    if (want >= 2 && blocks >= 2) return tiles_go<TYPE, MODE, 2>(a, st);
-    return tiles_go<TYPE, MODE, 1>(a, st);
+    // (16 waves fit 1024 threads' 128 registers a lane only for the plain products of 8 tokens)
+    if constexpr (MODE != TILES_GLU && TOK == 8)
+        if (want >= 16 && blocks >= 32) return tiles_go<TYPE, MODE, 16, TOK>(a, st);
+    if (want >= 8 && blocks >= 16) return tiles_go<TYPE, MODE, 8, TOK>(a, st);
+    if (want >= 4 && blocks >= 8) return tiles_go<TYPE, MODE, 4, TOK>(a, st);
+    if (want >= 2 && blocks >= 2) return tiles_go<TYPE, MODE, 2, TOK>(a, st);
+    return tiles_go<TYPE, MODE, 1, TOK>(a, st);
+}
+
+// 3..8 tokens keep four result registers a lane, 9..16 eight
+template <int TYPE, int MODE>
+static int tiles_t(TileArgs& a, hipStream_t st) {
+    return a.tokens <= 8 ? tiles_s<TYPE, MODE, 8>(a, st) : tiles_s<TYPE, MODE, 16>(a, st);
 }
 
 bool tiles_fits(int type, int cols, int tokens, const void* const* ws, int count) {
     // Q4_K only: Q6_K's 210-byte blocks load faster staged through LDS (the mmv kernels)
-    if (tokens < 3 || tokens > 8 || type != Q4_K || cols % 256 != 0) return false;
+    if (tokens < 3 || tokens > 16 || type != Q4_K || cols % 256 != 0) return false;
     // the tokens' scale tables in LDS (160 KB a workgroup on gfx950)
-    if ((size_t)2 * 8 * (cols / GROUP) * 4 > TILES_MAX_LDS) return false;
+    if ((size_t)2 * (tokens <= 8 ? 8 : 16) * (cols / GROUP) * 4 > TILES_MAX_LDS) return false;
     for (int i = 0; i < count; i++)
         if ((uintptr_t)ws[i] % 16 != 0) return false;
     return true;
@@ -313,9 +327,9 @@ int tiles_launch(int type, int mode, TileArgs& a, hipStream_t st) {
     a.tile_start[a.count] = total;
 #define LEAT_TILES_MODES(T)                                                 \
     switch (mode) {                                                         \
-    case TILES_PLAIN: return tiles_s<T, TILES_PLAIN>(a, st);                \
-    case TILES_RESIDUAL: return tiles_s<T, TILES_RESIDUAL>(a, st);          \
-    default: return tiles_s<T, TILES_GLU>(a, st);                           \
+    case TILES_PLAIN: return tiles_t<T, TILES_PLAIN>(a, st);                \
+    case TILES_RESIDUAL: return tiles_t<T, TILES_RESIDUAL>(a, st);          \
+    default: return tiles_t<T, TILES_GLU>(a, st);                           \
     }
     switch (type) {
     case Q4_K: LEAT_TILES_MODES(Q4_K)

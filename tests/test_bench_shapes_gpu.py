@@ -99,9 +99,10 @@ def test_glu_self_quantized_bench_shape(cuda, tokens):
     np.testing.assert_array_equal(host(hs), ws)
 
 
-@pytest.mark.parametrize("tokens", [3, 8])
+@pytest.mark.parametrize("tokens", [3, 8, 16])
 def test_glu_q8_bench_shape(cuda, tokens):
-    # leat_glu_matvec_q8 (the B=8 launch: the matrix-core tile kernel writing its outputs' q8)
+    # leat_glu_matvec_q8 (the B=8 and B=16 launches: the matrix-core tile kernel writing its
+    # outputs' q8)
     gate, g_dense = _matrix("gate", 0)
     up, u_dense = _matrix("gate", 1)
     rows, cols = g_dense.shape
