@@ -22,6 +22,7 @@
 #include "leatmi.h"
 #include "mmv.h"
 #include "prefill.h"
+#include "tiles.h"
 
 namespace leat {
 
@@ -385,6 +386,30 @@ static int few_launch(int type, int mode, const void* const* ws, int count, int 
     return mmv_launch(type, mode, m, st);
 }
 
+// the few-token gate+up GLU of Q4_K on the matrix-core tile kernels (3..16 tokens), which also
+// write the outputs' q8 when hq is given: faster than the LDS-staged ones for the GLU
+static bool few_tiles(int type, int cols, int tokens, const void* const* ws) {
+    return type == Q4_K && tokens <= FEW_TOKENS && tiles_fits(type, cols, tokens, ws, 2);
+}
+
+static int few_tiles_glu(const void* const* ws, int rows, int cols, const int32_t* xq, const float* xd,
+                         const float* xs, int tokens, int kind, float* out, int32_t* hq, float* hd, float* hs,
+                         hipStream_t st) {
+    constexpr int TILES_GLU_MODE = 2;
+    TileArgs t = {};
+    t.w[0] = (const uint8_t*)ws[0];
+    t.w[1] = (const uint8_t*)ws[1];
+    t.out[0] = out;
+    t.rows[0] = rows;
+    t.count = 1;
+    t.cols = cols;
+    t.tokens = tokens;
+    t.xq = xq, t.xd = xd, t.xs = xs;
+    t.kind = kind;
+    t.hq = (uint32_t*)hq, t.hd = hd, t.hs = hs;
+    return tiles_launch(Q4_K, TILES_GLU_MODE, t, st);
+}
+
 // the workspace a product would split into (0: it does not split)
 static int64_t workspace_of(int type, int rows, int cols, int tokens, bool gated) {
     if (tokens <= FEW_TOKENS) return 0;  // the decode kernels (few_launch) take no workspace
@@ -470,6 +495,8 @@ extern "C" int leat_glu_matmul(int type, const void* gate, const void* up, int r
         return -1;
     LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul: unknown GLU kind %d", kind);
     const void* ws[2] = {gate, up};
+    if (few_tiles(type, cols, tokens, ws))
+        return few_tiles_glu(ws, rows, cols, xq, xd, xs, tokens, kind, out, nullptr, nullptr, nullptr, (hipStream_t)stream);
     if (few_fits(type, cols, tokens, ws, 2))
         return few_launch(type, MMV_GLU, ws, 2, rows, cols, xq, xd, xs, tokens, nullptr, kind, out, (hipStream_t)stream);
     if (type == Q4_K)
@@ -491,6 +518,13 @@ extern "C" int leat_glu_matmul_q8(int type, const void* gate, const void* up, in
     LEAT_REQUIRE(hq && hd && hs && rows % GROUP == 0 && (uintptr_t)hq % 16 == 0,
                  "glu_matmul_q8: the q8 output needs d, s, rows in 32s and 16-byte aligned words");
     const void* ws[2] = {gate, up};
+    // 3..16 tokens of Q4_K: the tile kernel writes the q8 itself
+    if (few_tiles(type, cols, tokens, ws)) {
+        if (mmq_check(type, gate, rows, cols, xq, xd, xs, tokens, hd) || mmq_check(type, up, rows, cols, xq, xd, xs, tokens, hd))
+            return -1;
+        LEAT_REQUIRE(kind >= GLU_SILU && kind <= GLU_OAI, "glu_matmul_q8: unknown GLU kind %d", kind);
+        return few_tiles_glu(ws, rows, cols, xq, xd, xs, tokens, kind, out, hq, hd, hs, (hipStream_t)stream);
+    }
     // few tokens (with the f32 output given), and types the Q4_K kernel does not take: the GLU,
     // then the quantizer on its f32 outputs
     if (type != Q4_K || (out && few_fits(type, cols, tokens, ws, 2))) {
