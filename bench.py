@@ -361,13 +361,13 @@ def measure_decode(torch, model, steps, device, positions=(1, 4096)):
                               "hbm_frac": round((w_bytes + kv) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}  # fmt: skip
     # FlashDecoding alone (partial sums and their combine) over every layer's cache at the last
     # positions: the keys and values of (pos + 1) positions a layer, read once
-    from leat_amd import ops
+    from leat_amd import kernels, ops
 
     pos = positions[-1] - 1
     q = torch.randn(1, c.heads, 1, c.head_dim, device=device)
     slots = torch.zeros(1, dtype=torch.int32, device=device)
     lengths = torch.full((1,), pos + 1, dtype=torch.int32, device=device)
-    work = model._attention_workspace(1)
+    work = kernels.attention_workspace(1, c.heads, c.context, device)
     att_us = _graph_us(torch, lambda: [ops.attention(q, cache, None, c.head_dim**-0.5, slots, lengths, c.context, work)
                                        for cache in model.cache], steps) / c.layers  # fmt: skip
     att_bytes = (pos + 1) * 2 * c.kv_heads * c.head_dim * 2 + c.heads * c.head_dim * 4 * 2
@@ -379,8 +379,6 @@ def measure_decode(torch, model, steps, device, positions=(1, 4096)):
                                      "frac": att_gbs / HBM_PEAK_GBS, "traffic": att_traffic, "traffic_source": att_note}}  # fmt: skip
     # the largest single product of a step: the Q6_K head (RMSNorm + quantize once, then the
     # product: kernels.matvecs' path for launches of more than SELF_QUANTIZED_ROWS rows)
-    from leat_amd import kernels
-
     x = torch.randn(1, 1, c.dim, device=device)
     norm = (model.weights.output_norm, c.norm_eps)
     head_us = _graph_us(torch, lambda: kernels.matvecs(x, model.weights.output, norm=norm), steps)

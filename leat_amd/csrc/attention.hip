@@ -115,9 +115,9 @@ __device__ __forceinline__ float transpose_sum16(float (&v)[16], int lane) {
 }
 
 // A workgroup per (row, kv head, chunk): its waves take ATT_WAVE_KEYS keys each a round, from key
-// chunk * ATT_KEYS + 32 w, then every chunks * ATT_KEYS keys on. Lane l holds dimensions 2l, 2l + 1
+// chunk * ATT_KEYS + ATT_WAVE_KEYS w, then every chunks * ATT_KEYS keys on. Lane l holds dimensions 2l, 2l + 1
 // of the group's queries (scaled by scale * log2 e, so scores are in log2 units) and reads the
-// same two of each key: every key is one coalesced 256-byte read. The keys' 32 partial dot
+// same two of each key: every key is one coalesced 256-byte read. The keys' partial dot
 // products of each lane are summed across the wave by transpose_sum16, the scores go through LDS
 // to lanes a key each for the online softmax, and the weighted values are summed with lanes
 // again a pair of dimensions (a key's values one coalesced 256-byte read). The waves merge
@@ -201,7 +201,9 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
         }
     }
     // merge the waves: each leaves its (sums, max, total) in LDS; the workgroup's partial is
-    // the waves' sums rescaled to their common maximum
+    // the waves' sums rescaled to their common maximum. A row whose keys fit one chunk is done
+    // here: chunk 0 writes its sums over their total, the combine's arithmetic for one chunk
+    // (a weight of exactly 1), and the combine skips the row.
 #pragma unroll
     for (int h = 0; h < G; h++) {
         merge[w][h][2 * lane] = acc[h][0];
@@ -209,6 +211,8 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
         if (lane == 0) merge[w][h][ATT_DIM] = m[h], merge[w][h][ATT_DIM + 1] = l[h];
     }
     __syncthreads();
+    const bool alone = (length + ATT_KEYS - 1) / ATT_KEYS <= 1;  // no keys, or all in chunk 0
+    if (alone && chunk != 0) return;
     for (int i = threadIdx.x; i < G * (ATT_DIM + 2); i += ATT_WAVES * 64) {
         const int h = i / (ATT_DIM + 2), d = i % (ATT_DIM + 2);
         float top = NEG;
@@ -221,7 +225,15 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
 #pragma unroll
             for (int v = 0; v < ATT_WAVES; v++) y += exp2f(merge[v][h][ATT_DIM] - top) * merge[v][h][d];
         }
-        a.partial[(((int64_t)row * a.heads + h0 + h) * a.chunks + chunk) * (ATT_DIM + 2) + d] = y;
+        if (!alone) {
+            a.partial[(((int64_t)row * a.heads + h0 + h) * a.chunks + chunk) * (ATT_DIM + 2) + d] = y;
+        } else if (d < ATT_DIM) {
+            float total = 0.0f;
+#pragma unroll
+            for (int v = 0; v < ATT_WAVES; v++) total += exp2f(merge[v][h][ATT_DIM] - top) * merge[v][h][ATT_DIM + 1];
+            const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+            a.out[((int64_t)row * a.heads + h0 + h) * ATT_DIM + d] = y * inv;
+        }
     }
 }
 
@@ -238,6 +250,7 @@ __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kern
     const int slot = a.slots[row];
     const int length = slot >= 0 && slot < a.cache_slots ? min(a.lengths[row], a.cache_positions) : 0;
     const int live = min(a.chunks, (length + ATT_KEYS - 1) / ATT_KEYS);
+    if (live <= 1) return;  // the partial kernel's chunk 0 wrote the row
     const float* p = a.partial + (int64_t)rh * a.chunks * (ATT_DIM + 2);
     const float mine = lane < live ? p[lane * (ATT_DIM + 2) + ATT_DIM] : NEG;
     const float top = wave_max_dpp(mine);
