@@ -189,8 +189,9 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // of them run at once than sharing a pass between members does.
 // 1. threads 0..255 load the token's x (and the norm weight) into registers before anything
 //    else, so that its norm and quantization never wait behind the weight loads;
-// 2. its 8 waves route every token (route_token, the routing kernel's arithmetic) into LDS, and
-//    workgroup (0, 0) publishes ids and weights for the down product;
+// 2. wave 0 routes the pair's token (route_token, the routing kernel's arithmetic) into LDS, and
+//    the first row tile of each token's first pair publishes its ids and weights for the down
+//    product (routing every token in every workgroup cost 5.7 us of a B=8 launch);
 // 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
 //    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes x into
 //    LDS with the standalone quantizer's arithmetic (q8.h);
@@ -227,15 +228,15 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     constexpr int RPW = MOE_TILE / MOE_WAVES;
     constexpr int P = NT == 1 ? RPW : NT == 2 ? 2 : 1;  // rows of loads in flight
     extern __shared__ uint32_t moe_lds[];  // the token's q8 row: words, then d, then s
-    __shared__ int route_id[MOE_MAX_TOKENS * MOE_MAX_USED];
-    __shared__ float route_w[MOE_MAX_TOKENS * MOE_MAX_USED];
+    __shared__ int route_id[MOE_MAX_USED];
+    __shared__ float route_w[MOE_MAX_USED];
     __shared__ float partial[MOE_WAVES];
     __shared__ float glu_out[MOE_TILE];
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int p = blockIdx.y, row_base = blockIdx.x * MOE_TILE;
-    const int cols = a.cols, used = a.used, pairs = a.tokens * used;
+    const int cols = a.cols, used = a.used;
 
     // 1. the token's x, first in every wave's queue of loads (up to 8192 values: longer rows
     // would spill the registers, and load theirs after the weights)
@@ -245,17 +246,20 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     RowsInRegs<1, EARLY_X ? NX : 1> xin;
     if (EARLY_X) xin.load(xr, a.norm, cols);
 
-    // 2. routing
-    for (int t = w; t < a.tokens; t += MOE_WAVES) {
+    // 2. routing of the pair's token
+    const int token = p / used, slot = p - token * used;
+    if (w == 0) {
         int id;
         float weight;
-        route_token<EPL>(a.scores + (int64_t)t * a.experts, a.experts, used, lane, &id, &weight);
-        if (lane < used) route_id[t * used + lane] = id, route_w[t * used + lane] = weight;
+        route_token<EPL>(a.scores + (int64_t)token * a.experts, a.experts, used, lane, &id, &weight);
+        if (lane < used) route_id[lane] = id, route_w[lane] = weight;
     }
     __syncthreads();
-    if (blockIdx.x == 0 && p == 0)
-        for (int i = threadIdx.x; i < pairs; i += MOE_WAVES * 64) a.ids[i] = route_id[i], a.weights[i] = route_w[i];
-    const int e = route_id[p];  // route_token ids are always below `experts`
+    if (blockIdx.x == 0 && slot == 0 && (int)threadIdx.x < used) {
+        a.ids[(int64_t)token * used + threadIdx.x] = route_id[threadIdx.x];
+        a.weights[(int64_t)token * used + threadIdx.x] = route_w[threadIdx.x];
+    }
+    const int e = route_id[slot];  // route_token ids are always below `experts`
 
     // 3. the rows' loads, then the token's activations
     const int row0 = row_base + w;  // the wave's rows: row0 + 8r
