@@ -3,9 +3,9 @@
 //
 // Work split: lane l of a wave owns the same tasks of every row (tasks l, l + 64, ...; a task is
 // 32 weights of Q4_K or Q6_K, 64 of Q8_0, as in blocks.h), so it loads its activation words and
-// scales into registers once and reuses them for every row the wave streams. Rows of 14336
-// weights (seven turns of a wave's tasks) are split by columns instead: each of 7 waves takes one
-// turn of the same few rows (rows_split_kernel). A wave owns RPW
+// scales into registers once and reuses them for every row the wave streams. Rows of more than
+// four turns of a wave's tasks (10240 to 32768 weights: 14336 has seven) are split by columns
+// instead: each wave of a workgroup takes one turn of the same few rows (rows_split_kernel). A wave owns RPW
 // consecutive rows (of each matrix of the launch: gate and up for the GLU) and walks them one at
 // a time, the loads of the next rows (up to 4) in flight while the current row is computed. A row's sum
 // is one wave-wide DPP reduction.
@@ -196,40 +196,41 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
-constexpr int ROWS_SPLIT_P = 2;  // rows of loads a wave has in flight when long rows are split by columns
-
-// Long rows (more than 4 turns of a wave's tasks: Q6_K or Q4_K rows of 14336 weights, 7 turns)
-// split by columns: wave w of the KS waves of a workgroup takes turn w of every row, tasks
-// 64w + lane, so each lane holds one task's activations and streams the workgroup's R rows with P
-// of them in flight; the waves' partial sums of a row meet in LDS and are added in wave order.
-template <int TYPE, int B, int KS, int R, int MODE>
+// Long rows (more than 4 turns of a wave's tasks, up to 16: Q6_K or Q4_K rows of 10240 to 32768
+// weights, such as 11008, 13824, 14336, 18944) split by columns: wave w of the KS waves of a
+// workgroup takes turn w of every row, tasks 64w + lane (a last turn may be partial, and waves past
+// the row's turns idle), so each lane holds one task's activations and streams the workgroup's R
+// rows with P of them in flight; the waves' partial sums of a row meet in LDS and are added in
+// wave order.
+template <int TYPE, int B, int KS, int R, int P, int MODE, bool FULL>
 __global__ __launch_bounds__(KS * 64) void rows_split_kernel(RowsArgs a) {
     using RT = RowTask<TYPE>;
-    constexpr int P = R < ROWS_SPLIT_P ? R : ROWS_SPLIT_P;
+    static_assert(P <= R, "rows in flight");
     __shared__ float part[KS][B][R];
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int cols = a.cols, rows = a.rows[0], row0 = blockIdx.x * R;
     const uint32_t row_bytes = (uint32_t)(cols / Task<TYPE>::WEIGHTS) * Task<TYPE>::BYTES;
     const int task = WAVE * w + lane;
-    const typename RT::Off off = RT::at(task);
+    const bool has = FULL || task < cols / Task<TYPE>::TASK_W;  // the lane's task lies in the row (FULL: KS whole turns)
+    const typename RT::Off off = RT::at(has ? task : 0);
 
-    typename RT::Raw buf[P];
+    typename RT::Raw buf[P]{};  // lanes past the row's tasks keep zeros and add nothing
     auto fetch = [&](typename RT::Raw& dst, int row) {
-        dst = RT::load(a.w[0] + (size_t)min(row, rows - 1) * row_bytes, off);  // rows past the end: never stored
+        if (has) dst = RT::load(a.w[0] + (size_t)min(row, rows - 1) * row_bytes, off);  // rows past the end: never stored
     };
 #pragma unroll
     for (int p = 0; p < P; p++) fetch(buf[p], row0 + p);
     ActQ act[B];
 #pragma unroll
-    for (int t = 0; t < B; t++) act[t] = RT::act(load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, task), lane);
+    for (int t = 0; t < B; t++) act[t] = RT::act(load_act<TYPE>(a.xq, a.xd, a.xs, cols, t, has ? task : 0), lane);
 
     float sum[B][R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float acc[B];
 #pragma unroll
-        for (int t = 0; t < B; t++) acc[t] = RT::dot(buf[r % P], off, act[t]);
+        for (int t = 0; t < B; t++) acc[t] = has ? RT::dot(buf[r % P], off, act[t]) : 0.0f;
         if (r + P < R) fetch(buf[r % P], row0 + r + P);
 #pragma unroll
         for (int t = 0; t < B; t++) sum[t][r] = wave_sum_dpp(acc[t]);
@@ -273,7 +274,6 @@ static int rows_go(RowsArgs& a, hipStream_t st) {
 
 constexpr int ROWS_RPW = 2;      // rows a wave streams in the plain and residual products
 constexpr int ROWS_WPG = 8;      // waves per workgroup in the plain and residual products
-constexpr int ROWS_SPLIT_R = 2;  // rows a workgroup streams when long rows are split by columns (more, fewer workgroups: slower)
 constexpr int ROWS_GLU_WPG = 8;  // waves per workgroup of the GLU: tiles of 32 rows, 32 / WPG per wave
 
 template <int TYPE, int B, int NT, int MODE>
@@ -281,6 +281,41 @@ static int rows_shape(RowsArgs& a, bool xf32, hipStream_t st) {
     constexpr int WPG = MODE == ROWS_GLU ? ROWS_GLU_WPG : ROWS_WPG;
     constexpr int RPW = MODE == ROWS_GLU ? 32 / WPG : ROWS_RPW;
     return xf32 ? rows_go<TYPE, B, NT, RPW, WPG, MODE, true>(a, st) : rows_go<TYPE, B, NT, RPW, WPG, MODE, false>(a, st);
+}
+
+// Rows a workgroup streams when long rows are split by columns, and of them the rows whose loads
+// a wave has in flight. Each lane's activations serve R rows, so more rows cut the activation
+// bytes read per weight byte (about 40 B of q8 words and scales a task against 18 B of Q4_K
+// weights, 26 of Q6_K); measured on 4096x11008 to 4096x28672: Q4_K 4 rows (all 4 in flight at 1
+// token, 2 at 2 tokens), Q6_K 4 rows with 2 in flight, except rows of exactly 7 whole turns
+// (14336 weights) at 1 token, where 2 rows measured 4% faster. 8 rows were slower everywhere but
+// one shape.
+template <int TYPE, int B, bool FULL7>
+constexpr int split_rows() {
+    return TYPE == Q6_K && B == 1 && FULL7 ? 2 : 4;
+}
+template <int TYPE, int B>
+constexpr int split_depth() {
+    return TYPE == Q4_K && B == 1 ? 4 : 2;
+}
+
+template <int TYPE, int B, int KS, bool FULL, int MODE>
+static int rows_split_at(RowsArgs& a, hipStream_t st) {
+    constexpr int R = split_rows<TYPE, B, FULL && KS == 7>(), P = split_depth<TYPE, B>() < R ? split_depth<TYPE, B>() : R;
+    RowsArgs one = a;
+    for (int i = 0; i < a.count; i++) {  // a launch per matrix
+        one.w[0] = a.w[i], one.out[0] = a.out[i], one.rows[0] = a.rows[i];
+        hipLaunchKernelGGL((rows_split_kernel<TYPE, B, KS, R, P, MODE, FULL>), dim3((a.rows[i] + R - 1) / R),
+                           dim3(KS * WAVE), 0, st, one);
+        if (check_launch("rows")) return -1;
+    }
+    return 0;
+}
+
+template <int TYPE, int B, int KS, int MODE>
+static int rows_split_go(RowsArgs& a, hipStream_t st) {
+    return a.cols / Task<TYPE>::TASK_W == KS * WAVE ? rows_split_at<TYPE, B, KS, true, MODE>(a, st)
+                                                    : rows_split_at<TYPE, B, KS, false, MODE>(a, st);
 }
 
 template <int TYPE, int B, int MODE>
@@ -293,19 +328,19 @@ static int rows_nt(RowsArgs& a, bool xf32, hipStream_t st) {
             set_error("rows: rows of %d tasks", tasks);
             return -1;
         } else {
-            if (xf32 || tasks != 7 * WAVE) {
-                set_error("rows: long rows of %d tasks take quantized input, 7 turns", tasks);
+            if (xf32 || tasks > 16 * WAVE) {
+                set_error("rows: long rows of %d tasks take quantized input, at most 16 turns", tasks);
                 return -1;
             }
-            constexpr int R = ROWS_SPLIT_R;
-            RowsArgs one = a;
-            for (int i = 0; i < a.count; i++) {  // a launch per matrix
-                one.w[0] = a.w[i], one.out[0] = a.out[i], one.rows[0] = a.rows[i];
-                hipLaunchKernelGGL((rows_split_kernel<TYPE, B, 7, R, MODE>), dim3((a.rows[i] + R - 1) / R), dim3(7 * WAVE),
-                                   0, st, one);
-                if (check_launch("rows")) return -1;
-            }
-            return 0;
+            // a wave a turn: the waves of the launch are the row's turns, rounded up
+            const int turns = (tasks + WAVE - 1) / WAVE;
+            if (turns <= 5) return rows_split_go<TYPE, B, 5, MODE>(a, st);
+            if (turns <= 6) return rows_split_go<TYPE, B, 6, MODE>(a, st);
+            if (turns <= 7) return rows_split_go<TYPE, B, 7, MODE>(a, st);
+            if (turns <= 8) return rows_split_go<TYPE, B, 8, MODE>(a, st);
+            if (turns <= 10) return rows_split_go<TYPE, B, 10, MODE>(a, st);
+            if (turns <= 12) return rows_split_go<TYPE, B, 12, MODE>(a, st);
+            return rows_split_go<TYPE, B, 16, MODE>(a, st);
         }
     }
     return rows_shape<TYPE, B, 4, MODE>(a, xf32, st);
@@ -318,8 +353,9 @@ static int rows_b(RowsArgs& a, int tokens, bool xf32, hipStream_t st) {
 
 bool rows_fits(int type, int cols, int tokens, bool glu) {
     if (tokens < 1 || tokens > ROWS_MAX_TOKENS) return false;
-    // rows of 7 turns of a wave's 32-weight tasks (14336 weights), split by columns: q8 input, no GLU
-    const bool split = !glu && cols == 7 * WAVE * 32;
+    // rows of 5..16 turns of a wave's 32-weight tasks (up to 32768 weights), split by columns: q8
+    // input, no GLU
+    const bool split = !glu && cols / 32 > 4 * WAVE && cols / 32 <= 16 * WAVE;
     if (type == Q4_K) return cols % 256 == 0 && (cols / 32 <= 4 * WAVE || split);
     if (type == Q8_0) return cols % 64 == 0 && cols / 64 <= 2 * WAVE;
     // Q6_K rows of whole 512s (block pairs: 4-byte aligned rows)
