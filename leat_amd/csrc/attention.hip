@@ -91,23 +91,65 @@ struct AttentionArgs {
 // 16 values of each lane summed over the wave's 64 lanes, transposed: lane l ends with the sum of
 // value ((l >> 2) & 15). Each step keeps half the values and adds the partner lane's other half,
 // so 16 sums over 64 lanes take 8 + 4 + 2 + 1 exchanges and 2 more within each quad of lanes.
-// The step sizes are template arguments so that every register index is a constant: a run-time
+// The exchanges stay in registers: across lane halves and rows of 16 by gfx950's permlane swaps
+// (one instruction trades a pair of registers' halves, leaving each lane its own value and its
+// partner's), within rows by DPP moves. The sums are the same additions in the same order as a
+// shuffle through LDS would make. The register indices are compile-time constants: a run-time
 // index into v would compile to a compare-and-select chain over the whole array.
+__device__ __forceinline__ float f32_of(uint32_t u) { return __uint_as_float(u); }
+
+// lanes of bit `MASK` (32 or 16) clear keep v[i] and add the partner's v[i]; lanes of it set keep
+// v[HALF + i] and add the partner's. permlane32_swap trades lanes 32..63 of its first operand
+// with lanes 0..31 of its second, permlane16_swap the odd rows of 16 of the first with the even
+// rows of the second: either way each lane ends with its kept value in one register and the
+// partner's in the other. (Each half of the returned pair is copied into a scalar before its
+// bits are read as a float.)
 template <int HALF, int MASK>
-__device__ __forceinline__ void transpose_step(float (&v)[16], int lane) {
+__device__ __forceinline__ void swap_step(float (&v)[16]) {
+#pragma unroll
+    for (int i = 0; i < HALF; i++) {
+        uint32_t lo, hi;
+        if constexpr (MASK == 32) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[HALF + i]), false, false);
+            lo = r[0], hi = r[1];
+        } else {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[HALF + i]), false, false);
+            lo = r[0], hi = r[1];
+        }
+        // lanes of bit MASK clear: lo = their v[i], hi = the partner's; set: lo = the partner's
+        // v[HALF + i], hi = their own. keep + give in either case (addition commutes exactly)
+        v[i] = f32_of(lo) + f32_of(hi);
+    }
+}
+
+// DPP within rows of 16: row_ror:8 reads lane l ^ 8; row_shl:4 reads lane l + 4, row_shr:4 lane
+// l - 4, so the lanes of bit 2 clear take the first and those of it set the second (lane l ^ 4)
+constexpr int DPP_ROW_SHL4 = 0x104, DPP_ROW_SHR4 = 0x114, DPP_ROW_ROR8 = 0x128;
+
+template <int HALF, int MASK>
+__device__ __forceinline__ void dpp_step(float (&v)[16], int lane) {
     const bool upper = lane & MASK;
 #pragma unroll
     for (int i = 0; i < HALF; i++) {
         const float keep = upper ? v[HALF + i] : v[i], give = upper ? v[i] : v[HALF + i];
-        v[i] = keep + __shfl_xor(give, MASK, WAVE);
+        const int g = __float_as_int(give);
+        float other;
+        if constexpr (MASK == 8) {
+            other = __int_as_float(__builtin_amdgcn_mov_dpp(g, DPP_ROW_ROR8, 0xF, 0xF, false));
+        } else {
+            const float up = __int_as_float(__builtin_amdgcn_mov_dpp(g, DPP_ROW_SHL4, 0xF, 0xF, false));
+            const float down = __int_as_float(__builtin_amdgcn_mov_dpp(g, DPP_ROW_SHR4, 0xF, 0xF, false));
+            other = upper ? down : up;
+        }
+        v[i] = keep + other;
     }
 }
 
 __device__ __forceinline__ float transpose_sum16(float (&v)[16], int lane) {
-    transpose_step<8, 32>(v, lane);
-    transpose_step<4, 16>(v, lane);
-    transpose_step<2, 8>(v, lane);
-    transpose_step<1, 4>(v, lane);
+    swap_step<8, 32>(v);
+    swap_step<4, 16>(v);
+    dpp_step<2, 8>(v, lane);
+    dpp_step<1, 4>(v, lane);
     float s = v[0];
     s += __shfl_xor(s, 1, WAVE);
     s += __shfl_xor(s, 2, WAVE);
@@ -129,9 +171,10 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row = blockIdx.z, kvh = blockIdx.y, chunk = blockIdx.x;
-    const int slot = a.slots[row];
-    // a slot outside the cache holds no keys; lengths past its positions stop at them
-    const int length = slot >= 0 && slot < a.cache_slots ? min(a.lengths[row], a.cache_positions) : 0;
+    // the row's slot and length, both asked for at once; a slot outside the cache holds no keys,
+    // and lengths past its positions stop at them
+    const int slot = a.slots[row], asked = a.lengths[row];
+    const int length = slot >= 0 && slot < a.cache_slots ? min(asked, a.cache_positions) : 0;
     const int h0 = kvh * G;
     const float qscale = a.scale * LOG2E;
     float qa[G], qb[G];
@@ -237,47 +280,73 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
     }
 }
 
-// A workgroup of ATT_COMBINE_WAVES waves per (row, query head). In every wave lane c takes chunk
-// c's max and sum (up to 64 chunks) and the wave finds the common maximum and the total weight;
-// then lane = dimensions 2 lane, 2 lane + 1, wave w sums the rescaled partials of chunks w,
-// w + ATT_COMBINE_WAVES, ..., and the waves' sums meet in LDS.
+// A workgroup of ATT_COMBINE_WAVES waves per (row, query head). Every load goes out at once (the
+// row's slot and length too), so the kernel waits for one round trip: lane c of every wave takes chunk c's max and sum (up to 64
+// chunks), and with lane = dimensions 2 lane, 2 lane + 1 wave w takes the partial sums of chunks
+// w, w + ATT_COMBINE_WAVES, .... The wave then finds the common maximum and the total weight by
+// DPP, rescales its chunks' sums, and the waves' sums meet in LDS.
 constexpr int ATT_COMBINE_WAVES = 4;
+static_assert(ATT_CHUNKS <= WAVE && ATT_CHUNKS % ATT_COMBINE_WAVES == 0, "a lane per chunk, whole spans");
 
+// SPAN: chunks a wave sums, at least chunks / ATT_COMBINE_WAVES
+template <int SPAN>
 __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kernel(AttentionArgs a) {
     __shared__ float2 sums[ATT_COMBINE_WAVES - 1][64];
     const int rh = blockIdx.x, row = rh / a.heads, lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int slot = a.slots[row];
-    const int length = slot >= 0 && slot < a.cache_slots ? min(a.lengths[row], a.cache_positions) : 0;
-    const int live = min(a.chunks, (length + ATT_KEYS - 1) / ATT_KEYS);
-    if (live <= 1) return;  // the partial kernel's chunk 0 wrote the row
+    // the partials of every chunk the workgroup may take, asked for before the row's slot and
+    // length (their addresses need neither), at indices clamped into the row's a.chunks entries
+    // so that no load waits on a branch; chunks past the live ones are masked below, so whatever
+    // an earlier call left there adds nothing
     const float* p = a.partial + (int64_t)rh * a.chunks * (ATT_DIM + 2);
-    const float mine = lane < live ? p[lane * (ATT_DIM + 2) + ATT_DIM] : NEG;
-    const float top = wave_max_dpp(mine);
-    const float f = lane < live ? exp2f(mine - top) : 0.0f;
+    const int top_chunk = a.chunks - 1;
+    // (max, sum) of chunk `lane`: adjacent floats at an 8-byte boundary (rows of 130 floats)
+    float2 mine = *(const float2*)(p + min(lane, top_chunk) * (ATT_DIM + 2) + ATT_DIM);
+    float2 v[SPAN];
+#pragma unroll
+    for (int i = 0; i < SPAN; i++) v[i] = *(const float2*)(p + min(w + ATT_COMBINE_WAVES * i, top_chunk) * (ATT_DIM + 2) + 2 * lane);
+    const int slot = a.slots[row], asked = a.lengths[row];
+    const int length = slot >= 0 && slot < a.cache_slots ? min(asked, a.cache_positions) : 0;
+    // a row of one live chunk was written by the partial kernel's chunk 0: the workgroup runs
+    // through (no branch for the loads above to sink below) and stores nothing
+    const int live = min(a.chunks, (length + ATT_KEYS - 1) / ATT_KEYS);
+    if (lane >= live) mine = make_float2(NEG, 0.0f);
+#pragma unroll
+    for (int i = 0; i < SPAN; i++)
+        if (w + ATT_COMBINE_WAVES * i >= live) v[i] = make_float2(0.0f, 0.0f);
+    const float top = wave_max_dpp(mine.x);
+    const float f = lane < live ? exp2f(mine.x - top) : 0.0f;  // chunk lane's weight, 0 past the live chunks
     float y0 = 0.0f, y1 = 0.0f;
-#pragma unroll 4
-    for (int c = w; c < live; c += ATT_COMBINE_WAVES) {
-        const float fc = __shfl(f, c, WAVE);
-        const float2 v = *(const float2*)(p + c * (ATT_DIM + 2) + 2 * lane);
-        y0 += fc * v.x, y1 += fc * v.y;
+#pragma unroll
+    for (int i = 0; i < SPAN; i++) {
+        const float fc = __shfl(f, w + ATT_COMBINE_WAVES * i, WAVE);
+        y0 += fc * v[i].x, y1 += fc * v[i].y;
     }
     if (w > 0) sums[w - 1][lane] = make_float2(y0, y1);
     __syncthreads();
     if (w > 0) return;
-    const float total = wave_sum_dpp(lane < live ? f * p[lane * (ATT_DIM + 2) + ATT_DIM + 1] : 0.0f);
+    const float total = wave_sum_dpp(f * mine.y);
 #pragma unroll
-    for (int v = 0; v < ATT_COMBINE_WAVES - 1; v++) y0 += sums[v][lane].x, y1 += sums[v][lane].y;
+    for (int i = 0; i < ATT_COMBINE_WAVES - 1; i++) y0 += sums[i][lane].x, y1 += sums[i][lane].y;
     const float inv = total > 0.0f ? 1.0f / total : 0.0f;
     float* o = a.out + (int64_t)row * a.heads * ATT_DIM + (int64_t)(rh % a.heads) * ATT_DIM;
-    *(float2*)(o + 2 * lane) = make_float2(y0 * inv, y1 * inv);
+    if (live > 1) *(float2*)(o + 2 * lane) = make_float2(y0 * inv, y1 * inv);
 }
 
 template <int G>
 static int attention_go(AttentionArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attention_partial_kernel<G>), dim3(a.chunks, a.kv_heads, a.rows), dim3(ATT_WAVES * 64), 0, st, a);
     if (check_launch("attention")) return -1;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(a.rows * a.heads), dim3(ATT_COMBINE_WAVES * 64), 0, st, a);
+    const dim3 grid(a.rows * a.heads), block(ATT_COMBINE_WAVES * 64);
+    const int span = (a.chunks + ATT_COMBINE_WAVES - 1) / ATT_COMBINE_WAVES;
+    if (span <= 2)
+        hipLaunchKernelGGL(attention_combine_kernel<2>, grid, block, 0, st, a);
+    else if (span <= 4)
+        hipLaunchKernelGGL(attention_combine_kernel<4>, grid, block, 0, st, a);
+    else if (span <= 8)
+        hipLaunchKernelGGL(attention_combine_kernel<8>, grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL(attention_combine_kernel<ATT_CHUNKS / ATT_COMBINE_WAVES>, grid, block, 0, st, a);
     return check_launch("attention combine");
 }
 

@@ -208,12 +208,19 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
             stage<MODE>(a, so, row0, tok0, full, lds0 + (uint32_t)((step + 1) & 1) * PF_BUF, first + step + 1, w);
 
         const uint32_t wl = buf + wo;
-        const u32x4 hdr = lds_read<u32x4>(wl);
-        const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
 
         // the step's mins, - dmin * m[row] * xs[token], on the matrix cores straight into the
         // sums: K = 2 is a pair of groups, 2j in lane half 0 and 2j + 1 in half 1. Issued first,
-        // so that their chain of products runs while the groups' pipeline fills
+        // so that their chain of products runs while the groups' pipeline fills; the 8 xs reads
+        // go out together, so their LDS latencies overlap instead of queueing one per product
+        float xsv[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int q = 0; q < 2; q++) xsv[j][q] = lds_read<float>(buf + (ts[q] ^ (8u * j)));
+        const u32x4 hdr = lds_read<u32x4>(wl);
+        const float d = f16_lo(hdr[0]), dmin = f16_hi(hdr[0]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int g = 2 * j + h;
@@ -222,7 +229,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 2) void prefill_q4k(PrefillArgs a) {
             const uint32_t mv = g < 4 ? (x1 & 63u) : (((x2 >> 4) & 15u) | ((x1 >> 2) & 0x30u));
             const float mn = -dmin * (float)mv;
 #pragma unroll
-            for (int q = 0; q < 2; q++) acc[q] = mfma_f32(lds_read<float>(buf + (ts[q] ^ (8u * j))), mn, acc[q]);
+            for (int q = 0; q < 2; q++) acc[q] = mfma_f32(xsv[j][q], mn, acc[q]);
         }
 
         // The step's 8 groups as a three-stage pipeline: the operands of group g + 2 are read from
