@@ -198,8 +198,11 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // 4. each wave streams 4 rows of gate and up against the activations in registers;
 // 5. the 32 rows are one group of 32, so the workgroup writes the hidden rows' q8 words, d and s
 //    as well as (optionally) their f32 values.
-// MOE_WAVES waves of a workgroup: 32 rows, 4 a wave
+// MOE_WAVES waves of a workgroup: MOE_TILE rows, 4 a wave (MOE_WIDE_TILE, 8 a wave, for
+// launches of at least MOE_WIDE_PAIRS pairs, whose many workgroups then share out each one's
+// routing and quantization over twice the weights)
 constexpr int MOE_WAVES = 8, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
+constexpr int MOE_WIDE_TILE = 64, MOE_WIDE_PAIRS = 32;
 
 struct MoeGluArgs {
     const uint8_t* gate;
@@ -222,20 +225,22 @@ struct MoeGluArgs {
     float* hs;
 };
 
-template <int TYPE, int NT, int EPL>
+template <int TYPE, int NT, int EPL, int TILE>
 __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     using RT = RowTask<TYPE>;
-    constexpr int RPW = MOE_TILE / MOE_WAVES;
-    constexpr int P = NT == 1 ? RPW : NT == 2 ? 2 : 1;  // rows of loads in flight
+    constexpr int RPW = TILE / MOE_WAVES;
+    // rows of loads in flight: all of a narrow tile's; one of a wide tile's, whose launches of many
+    // pairs keep more waves resident instead (measured fastest at 8 tokens of top-8)
+    constexpr int P = NT == 1 ? (TILE == MOE_TILE ? RPW : 1) : NT == 2 ? 2 : 1;
     extern __shared__ uint32_t moe_lds[];  // the token's q8 row: words, then d, then s
     __shared__ int route_id[MOE_MAX_USED];
     __shared__ float route_w[MOE_MAX_USED];
     __shared__ float partial[MOE_WAVES];
-    __shared__ float glu_out[MOE_TILE];
+    __shared__ float glu_out[TILE];
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int p = blockIdx.y, row_base = blockIdx.x * MOE_TILE;
+    const int p = blockIdx.y, row_base = blockIdx.x * TILE;
     const int cols = a.cols, used = a.used;
 
     // 1. the token's x, first in every wave's queue of loads (up to 8192 values: longer rows
@@ -316,10 +321,10 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
         }
     }
 
-    // 5. the 32 outputs quantized as one group (rows a multiple of 32)
+    // 5. the outputs quantized in groups of 32, a thread a row (rows a multiple of TILE)
     if (!a.hq) return;
     __syncthreads();
-    if ((int)threadIdx.x < MOE_TILE) {
+    if ((int)threadIdx.x < TILE) {
         const int i = threadIdx.x;
         const float v = glu_out[i];
         float amax = fabsf(v);
@@ -334,25 +339,31 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
         const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
         const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
         const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
-        const int64_t first = (int64_t)p * a.rows + row_base;
-        if ((i & 3) == 0) a.hq[(first + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        if (i == 0) {
+        const int64_t first = (int64_t)p * a.rows + row_base + (i & ~31);  // the group's first row
+        if ((i & 3) == 0) a.hq[(first + (i & 31)) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        if ((i & 31) == 0) {
             a.hd[first / GROUP] = scale;
             a.hs[first / GROUP] = scale * (float)total;
         }
     }
 }
 
-template <int TYPE, int NT>
-static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
-    const dim3 grid((a.rows + MOE_TILE - 1) / MOE_TILE, a.tokens * a.used);
+template <int TYPE, int NT, int TILE>
+static void moe_glu_tile(MoeGluArgs& a, hipStream_t st) {
+    const dim3 grid(a.rows / TILE, a.tokens * a.used);
     const size_t lds = (size_t)a.cols + 2 * (size_t)(a.cols / GROUP) * 4;
     if (a.experts <= WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 1>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 1, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
     else if (a.experts <= 2 * WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 2>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 2, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 4>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 4, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+}
+
+template <int TYPE, int NT>
+static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
+    if (a.tokens * a.used >= MOE_WIDE_PAIRS && a.rows % MOE_WIDE_TILE == 0) return moe_glu_tile<TYPE, NT, MOE_WIDE_TILE>(a, st);
+    moe_glu_tile<TYPE, NT, MOE_TILE>(a, st);
 }
 
 template <int TYPE>
