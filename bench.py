@@ -631,6 +631,49 @@ def _leg(r):
             "roofline": r["roofline"]}  # fmt: skip
 
 
+def measure_peaks(torch, device) -> dict:
+    """The rates this GPU reaches, beside the published peaks the rooflines divide by: a plain
+    streaming read of 2 GiB (far past the 256 MB MALL; the library's leat_probe_read, 16-byte
+    loads, 32 workgroups a CU; the fastest of 3 timings) and back-to-back int8 matrix-core products (leat_probe_mfma_i8:
+    4 independent v_mfma_i32_32x32x32_i8 chains a wave, 4 waves a SIMD; the fastest of 3). Each result is checked
+    against what the probe must return."""
+    from leat_amd import _lib
+
+    nbytes = 2 << 30
+    data = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+    groups = 32 * torch.cuda.get_device_properties(device).multi_processor_count
+    sink = torch.empty(groups, dtype=torch.int32, device=device)
+    # the stream is read at each launch (inside a graph capture it is the capture's own), and the
+    # sinks are cleared first, so a replay that ran nothing fails the checks below
+    read = lambda: _lib.call("leat_probe_read", data.data_ptr(), nbytes, sink.data_ptr(), groups, _lib.stream())
+    sink.zero_()
+    read_us = min(_graph_us(torch, read, 10) for _ in range(3))
+    if int(sink.to(torch.int64).sum().item()) % (1 << 32) != (nbytes // 4) % (1 << 32):
+        raise RuntimeError("probe_read: the word sum is not the buffer's")
+    del data
+    iters, mfma_groups = 4096, 4 * torch.cuda.get_device_properties(device).multi_processor_count
+    msink = torch.empty(4 * mfma_groups, dtype=torch.int32, device=device)
+    mfma = lambda: _lib.call("leat_probe_mfma_i8", iters, mfma_groups, msink.data_ptr(), _lib.stream())
+    msink.zero_()
+    mfma_us = min(_graph_us(torch, mfma, 10) for _ in range(3))
+    if not bool((msink == 128 * iters).all().item()):
+        raise RuntimeError("probe_mfma_i8: a wave's sums are not 128 x rounds")
+    ops = 4 * mfma_groups * iters * 4 * 65536
+    return {"hbm_read_gbs": round(nbytes / read_us / 1e3, 1), "hbm_read_bytes": nbytes,
+            "int8_mfma_tops": round(ops / mfma_us / 1e6, 1), "int8_mfma_ops": ops,
+            "published": {"hbm_gbs": HBM_PEAK_GBS, "int8_tops": INT8_PEAK_TOPS}}  # fmt: skip
+
+
+def _with_measured_peaks(node, peaks):
+    # every roofline of the line gains the measured rate of its bound beside the published peak
+    if isinstance(node, dict):
+        if node.get("bound") in ("hbm", "mfma") and "peak" in node:
+            node["peak_measured"] = peaks["hbm_read_gbs"] if node["bound"] == "hbm" else peaks["int8_mfma_tops"]
+        for v in node.values():
+            _with_measured_peaks(v, peaks)
+    return node
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -700,6 +743,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    peaks = measure_peaks(torch, device)
+    print(f"peaks: streaming read {peaks['hbm_read_gbs']:.0f} GB/s, int8 matrix cores {peaks['int8_mfma_tops']:.0f} TOPS",
+          file=sys.stderr, flush=True)  # fmt: skip
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
@@ -725,8 +771,9 @@ def main():
         "prefill": prefill,
         "moe": moe,
         "cpu_baseline": cpu,
+        "peaks_measured": peaks,
     }
-    print(json.dumps(line))
+    print(json.dumps(_with_measured_peaks(line, peaks)))
 
 
 if __name__ == "__main__":

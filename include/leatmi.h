@@ -270,6 +270,17 @@ int64_t leat_argmax_workspace(int rows);
 int leat_argmax(const float *x, int rows, int n, void *workspace, int64_t workspace_bytes,
                 int32_t *out, void *stream);
 
+/* Measurement probes, with no counterpart in leat: the rates this GPU reaches, reported beside the
+ * published peaks that the benchmark's rooflines divide by.
+ * leat_probe_read: streams `bytes` (whole 16-byte chunks, 16-byte aligned) with 16-byte loads and
+ * leaves in sink[g], for each of `workgroups` workgroups, its share of the sum of every 32-bit word
+ * modulo 2^32 (the sink values add up to the whole sum).
+ * leat_probe_mfma_i8: `workgroups` workgroups of 4 waves, each wave running `iters` rounds of 4
+ * independent v_mfma_i32_32x32x32_i8 on all-ones operands (65,536 ops each); sink[4 g + w] =
+ * 128 * iters. */
+int leat_probe_read(const void *data, int64_t bytes, uint32_t *sink, int workgroups, void *stream);
+int leat_probe_mfma_i8(int iters, int workgroups, int32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,8 @@ SIGNATURES: dict[str, list] = {
     "leat_attention": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i, _f, _p, _i64, _p, _p],
     "leat_argmax_workspace": [_i],
     "leat_argmax": [_p, _i, _i, _p, _i64, _p, _p],
+    "leat_probe_read": [_p, _i64, _p, _i, _p],
+    "leat_probe_mfma_i8": [_i, _i, _p, _p],
     "leat_glu_matvec_f32": [_i, _p, _p, _i, _i, _p, _i, _p, _f, _i, _p, _p, _p, _p, _p],
 }
 
