@@ -262,6 +262,17 @@ int leat_attention(const float *q, const void *cache, int cache_slots, int kv_he
                    const int32_t *lengths, int max_length, float scale, float *workspace,
                    int64_t workspace_bytes, float *out, void *stream);
 
+/* leat_attention that also writes the q8 of its output (no counterpart in leat, whose o product
+ * quantizes the attention output itself, leat/kernels/matvec.py:362-380 through
+ * leat/kernels/quantize.py:92-109): hq, hd, hs exactly what leat_quantize_q8 writes for the rows
+ * of heads * dim values in out, for the q8-input product that follows (leat_matvec). hq 4-byte
+ * aligned. */
+int leat_attention_q8(const float *q, const void *cache, int cache_slots, int kv_heads,
+                      int cache_positions, int dim, int rows, int heads, const int32_t *slots,
+                      const int32_t *lengths, int max_length, float scale, float *workspace,
+                      int64_t workspace_bytes, float *out, int32_t *hq, float *hd, float *hs,
+                      void *stream);
+
 /* The workspace bytes leat_argmax needs for `rows` rows. */
 int64_t leat_argmax_workspace(int rows);
 

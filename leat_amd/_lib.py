@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "leat_attention_workspace": [_i, _i, _i],
     "leat_qkv_rotate_f32": [_i, _p, _p, _p, _i, _i, _i, _i, _p, _i, _p, _f, _p, _p, _i, _p, _p, _p, _p, _i, _i, _p],
     "leat_attention": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i, _f, _p, _i64, _p, _p],
+    "leat_attention_q8": [_p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _i, _f, _p, _i64, _p, _p, _p, _p, _p],
     "leat_argmax_workspace": [_i],
     "leat_argmax": [_p, _i, _i, _p, _i64, _p, _p],
     "leat_probe_read": [_p, _i64, _p, _i, _p],

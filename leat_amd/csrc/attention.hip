@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "q8.h"
 
 namespace leat {
 
@@ -86,7 +87,27 @@ struct AttentionArgs {
     float scale;
     float* partial;  // (rows * heads, chunks, dim + 2): unnormalized output, then max (log2 units) and sum
     float* out;      // (rows, heads * dim)
+    // or null; else the q8 of out as leat_quantize_q8 writes a row of heads * dim values: words,
+    // then each group's d and s
+    uint32_t* hq;
+    float* hd;
+    float* hs;
 };
+
+// The q8 of 4 consecutive output values v at column `col` (a multiple of 4) of row `row`, by the
+// aligned octet of lanes that holds one group of 32 (the standalone quantizer's arithmetic,
+// quantize4): every lane of the octet takes part; `store` says whether this lane's word is kept.
+__device__ __forceinline__ void attention_q8(const AttentionArgs& a, float4 v, int row, int col, bool store) {
+    float dv, sv;
+    const uint32_t word = quantize4(v, &dv, &sv);
+    const int64_t at = (int64_t)row * a.heads * ATT_DIM + col;
+    if (!store) return;
+    a.hq[at / 4] = word;
+    if (col % GROUP == 0) {
+        a.hd[at / GROUP] = dv;
+        a.hs[at / GROUP] = sv;
+    }
+}
 
 // 16 values of each lane summed over the wave's 64 lanes, transposed: lane l ends with the sum of
 // value ((l >> 2) & 15). Each step keeps half the values and adds the partner lane's other half,
@@ -168,6 +189,7 @@ template <int G>
 __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(AttentionArgs a) {
     __shared__ float scores[ATT_WAVES][G][ATT_WAVE_KEYS];
     __shared__ float merge[ATT_WAVES][G][ATT_DIM + 2];
+    __shared__ float4 alone_out[G][ATT_DIM / 4];  // a single-chunk row's outputs, for their q8
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row = blockIdx.z, kvh = blockIdx.y, chunk = blockIdx.x;
@@ -276,7 +298,14 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
             for (int v = 0; v < ATT_WAVES; v++) total += exp2f(merge[v][h][ATT_DIM] - top) * merge[v][h][ATT_DIM + 1];
             const float inv = total > 0.0f ? 1.0f / total : 0.0f;
             a.out[((int64_t)row * a.heads + h0 + h) * ATT_DIM + d] = y * inv;
+            if (a.hq) ((float*)alone_out[h])[d] = y * inv;
         }
+    }
+    // the q8 of a single-chunk row's G heads: a thread a float4, an octet of threads a group
+    if (alone && a.hq) {
+        __syncthreads();
+        const int t = threadIdx.x, h = t / (ATT_DIM / 4), c = t % (ATT_DIM / 4);
+        if (t < G * (ATT_DIM / 4)) attention_q8(a, alone_out[h][c], row, (h0 + h) * ATT_DIM + 4 * c, true);
     }
 }
 
@@ -330,7 +359,17 @@ __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kern
     for (int i = 0; i < ATT_COMBINE_WAVES - 1; i++) y0 += sums[i][lane].x, y1 += sums[i][lane].y;
     const float inv = total > 0.0f ? 1.0f / total : 0.0f;
     float* o = a.out + (int64_t)row * a.heads * ATT_DIM + (int64_t)(rh % a.heads) * ATT_DIM;
-    if (live > 1) *(float2*)(o + 2 * lane) = make_float2(y0 * inv, y1 * inv);
+    const float2 y = make_float2(y0 * inv, y1 * inv);
+    if (live > 1) *(float2*)(o + 2 * lane) = y;
+    if (a.hq) {
+        // the head's q8: lanes 0..31 gather dimensions 4 lane .. 4 lane + 3 (held by lanes 2 lane
+        // and 2 lane + 1), and each octet of them quantizes one group; lanes 32.. take part in the
+        // octet reductions of their own rows and store nothing
+        const float2 lo = make_float2(__shfl(y.x, 2 * lane, WAVE), __shfl(y.y, 2 * lane, WAVE));
+        const float2 hi = make_float2(__shfl(y.x, 2 * lane + 1, WAVE), __shfl(y.y, 2 * lane + 1, WAVE));
+        attention_q8(a, make_float4(lo.x, lo.y, hi.x, hi.y), row, (rh % a.heads) * ATT_DIM + 4 * lane,
+                     live > 1 && lane < ATT_DIM / 4);
+    }
 }
 
 template <int G>
@@ -380,10 +419,10 @@ extern "C" int64_t leat_attention_workspace(int rows, int heads, int max_length)
     return (int64_t)rows * heads * attention_chunks(max_length) * (ATT_DIM + 2) * 4;
 }
 
-extern "C" int leat_attention(const float* q, const void* cache, int cache_slots, int kv_heads, int cache_positions,
-                              int dim, int rows, int heads, const int32_t* slots, const int32_t* lengths,
-                              int max_length, float scale, float* workspace, int64_t workspace_bytes, float* out,
-                              void* stream) {
+static int attention_launch(const float* q, const void* cache, int cache_slots, int kv_heads, int cache_positions,
+                            int dim, int rows, int heads, const int32_t* slots, const int32_t* lengths, int max_length,
+                            float scale, float* workspace, int64_t workspace_bytes, float* out, uint32_t* hq,
+                            float* hd, float* hs, void* stream) {
     LEAT_REQUIRE(q && cache && slots && lengths && workspace && out, "attention: null pointer");
     LEAT_REQUIRE(dim == ATT_DIM, "attention: heads of %d dimensions (this kernel takes %d)", dim, ATT_DIM);
     LEAT_REQUIRE(kv_heads > 0 && heads % kv_heads == 0, "attention: %d query heads over %d kv heads", heads, kv_heads);
@@ -398,7 +437,7 @@ extern "C" int leat_attention(const float* q, const void* cache, int cache_slots
                  (long long)leat_attention_workspace(rows, heads, max_length));
     if (rows == 0) return 0;
     AttentionArgs a = {q, (const _Float16*)cache, cache_slots, kv_heads, cache_positions, rows, heads, group, slots,
-                       lengths, attention_chunks(max_length), scale, workspace, out};
+                       lengths, attention_chunks(max_length), scale, workspace, out, hq, hd, hs};
     hipStream_t st = (hipStream_t)stream;
     switch (group) {
     case 1: return attention_go<1>(a, st);
@@ -406,4 +445,22 @@ extern "C" int leat_attention(const float* q, const void* cache, int cache_slots
     case 4: return attention_go<4>(a, st);
     default: return attention_go<8>(a, st);
     }
+}
+
+extern "C" int leat_attention(const float* q, const void* cache, int cache_slots, int kv_heads, int cache_positions,
+                              int dim, int rows, int heads, const int32_t* slots, const int32_t* lengths,
+                              int max_length, float scale, float* workspace, int64_t workspace_bytes, float* out,
+                              void* stream) {
+    return attention_launch(q, cache, cache_slots, kv_heads, cache_positions, dim, rows, heads, slots, lengths,
+                            max_length, scale, workspace, workspace_bytes, out, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int leat_attention_q8(const float* q, const void* cache, int cache_slots, int kv_heads, int cache_positions,
+                                 int dim, int rows, int heads, const int32_t* slots, const int32_t* lengths,
+                                 int max_length, float scale, float* workspace, int64_t workspace_bytes, float* out,
+                                 int32_t* hq, float* hd, float* hs, void* stream) {
+    LEAT_REQUIRE(hq && hd && hs, "attention_q8: null q8 output");
+    LEAT_REQUIRE((uintptr_t)hq % 4 == 0, "attention_q8: q8 words 4-byte aligned");
+    return attention_launch(q, cache, cache_slots, kv_heads, cache_positions, dim, rows, heads, slots, lengths,
+                            max_length, scale, workspace, workspace_bytes, out, (uint32_t*)hq, hd, hs, stream);
 }

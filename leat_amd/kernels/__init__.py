@@ -18,6 +18,7 @@ from leat_amd import _lib
 from leat_amd.kernels.attention import (
     argmax,
     attention,
+    attention_q8,
     attention_workspace,
     embedding,
     rotate,
@@ -182,6 +183,32 @@ def matvecs(
         _lib.call("leat_matvec", int(w.type), _blocks(w), w.shape[0], cols, xq.data_ptr(), xd.data_ptr(),
                   xs.data_ptr(), tokens, add.data_ptr(), out.data_ptr(), _lib.stream(device))  # fmt: skip
     return [out.view(*lead, w.shape[0]) for out, w in zip(outs, ws, strict=True)]
+
+
+def matvecs_quantized(
+    q8: Q8, tokens: int, cols: int, *ws: QTensor, residual: torch.Tensor | None = None
+) -> list[torch.Tensor]:
+    """matvecs() of activations already quantized as quantize_q8 makes them, (words, d, s) of
+    `tokens` rows of `cols` values (attention_q8's output): the same products, bit for bit, as
+    matvecs of the f32 rows those came from, without quantizing them again. Returns (tokens,
+    rows) f32 for each w."""
+    if residual is not None and len(ws) != 1:
+        raise ValueError("matvecs adds a residual to the product of one matrix only")
+    xq, xd, xs = q8
+    device = xq.device
+    outs = [torch.empty(tokens * w.shape[0], dtype=torch.float32, device=device) for w in ws]
+    if residual is None:
+        n = len(ws)
+        _lib.call("leat_matvecs", n, (ctypes.c_int * n)(*(int(w.type) for w in ws)),
+                  (ctypes.c_void_p * n)(*(_blocks(w) for w in ws)), (ctypes.c_int * n)(*(w.shape[0] for w in ws)),
+                  cols, xq.data_ptr(), xd.data_ptr(), xs.data_ptr(), tokens,
+                  (ctypes.c_void_p * n)(*(o.data_ptr() for o in outs)), _lib.stream(device))  # fmt: skip
+    else:
+        w, out = ws[0], outs[0]
+        add = _f32(residual).reshape(-1)
+        _lib.call("leat_matvec", int(w.type), _blocks(w), w.shape[0], cols, xq.data_ptr(), xd.data_ptr(),
+                  xs.data_ptr(), tokens, add.data_ptr(), out.data_ptr(), _lib.stream(device))  # fmt: skip
+    return [out.view(tokens, w.shape[0]) for out, w in zip(outs, ws, strict=True)]
 
 
 def supports_qkv_rotate(x: torch.Tensor, q: QTensor, k: QTensor, v: QTensor, cache: torch.Tensor, halves: bool,
@@ -553,9 +580,9 @@ def mixture(
 
 
 __all__ = [
-    "argmax", "attention", "attention_workspace", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
+    "argmax", "attention", "attention_q8", "attention_workspace", "embedding", "rotate", "supports_argmax", "supports_attention", "supports_embedding",
     "supports_rotate",
     "FEW_TOKENS", "GROUP", "MATVEC_TOKENS", "MAX_PAIRS", "MAX_USED", "SELF_QUANTIZED_ROWS", "SELF_QUANTIZED_TOKENS", "feed_forward", "group_dots", "matmul_fits", "matmuls", "qkv_rotate", "supports_qkv_rotate",
-    "matvec_f32x", "matvecs", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
+    "matvec_f32x", "matvecs", "matvecs_quantized", "mixture", "quantize_q8", "route", "scores", "supports_matmul", "supports_matvec",
     "supports_mixture", "supports_scores", "swiglu",
 ]  # fmt: skip

@@ -94,6 +94,21 @@ def attention(
     D), scores q.k * scale. `max_length` bounds every length (the cache's positions if not
     given) and sizes the launch. `workspace` is one from attention_workspace() for at least these
     rows, heads and max_length (a new one is made if not given). Returns (1, T, H * D) f32."""
+    out, _ = _attention(q, cache, slots, lengths, scale, max_length, workspace, False)
+    return out
+
+
+def attention_q8(
+    q: torch.Tensor, cache: torch.Tensor, slots, lengths, scale: float, max_length: int | None = None,
+    workspace: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:  # fmt: skip
+    """attention(), and the q8 of its output as quantize_q8 would make it of the (T, H * D) rows,
+    written by the attention kernels themselves (include/leatmi.h leat_attention_q8): for the
+    q8-input product that follows."""
+    return _attention(q, cache, slots, lengths, scale, max_length, workspace, True)
+
+
+def _attention(q, cache, slots, lengths, scale, max_length, workspace, q8: bool):
     _lib.require_device(q)
     _, heads, rows, dim = q.shape
     _, cache_slots, kv_heads, cache_positions, _ = cache.shape
@@ -107,13 +122,20 @@ def attention(
         if work.dtype != torch.uint8 or not work.is_contiguous() or work.numel() < size or work.device != device:
             raise _lib.LeatError("attention: the workspace is not one of attention_workspace() for these rows")
         size = work.numel() // 4 * 4
-    out = torch.empty(rows * heads * dim, dtype=torch.float32, device=device)
+    n = rows * heads * dim
+    out = torch.empty(n, dtype=torch.float32, device=device)
     src = q.float().contiguous()
     slot_rows, length_rows = _rows_tensor(slots, device), _rows_tensor(lengths, device)
-    _lib.call("leat_attention", src.data_ptr(), cache.data_ptr(), cache_slots, kv_heads, cache_positions, dim, rows,
-              heads, slot_rows.data_ptr(), length_rows.data_ptr(), longest, float(scale), work.data_ptr(), size,
-              out.data_ptr(), _lib.stream(device))  # fmt: skip
-    return out.view(1, rows, heads * dim)
+    args = (src.data_ptr(), cache.data_ptr(), cache_slots, kv_heads, cache_positions, dim, rows, heads,
+            slot_rows.data_ptr(), length_rows.data_ptr(), longest, float(scale), work.data_ptr(), size, out.data_ptr())  # fmt: skip
+    packed = None
+    if q8:
+        packed = (torch.empty(n // 4, dtype=torch.int32, device=device), torch.empty(n // 32, dtype=torch.float32, device=device),
+                  torch.empty(n // 32, dtype=torch.float32, device=device))  # fmt: skip
+        _lib.call("leat_attention_q8", *args, *(t.data_ptr() for t in packed), _lib.stream(device))
+    else:
+        _lib.call("leat_attention", *args, _lib.stream(device))
+    return out.view(1, rows, heads * dim), packed
 
 
 def supports_argmax(x: torch.Tensor) -> bool:

@@ -235,8 +235,8 @@ class Model:
         for layer, cache in zip(w.layers, self.cache, strict=True):
             q_rot = ops.qkv_rotate(x, layer.q, layer.k, layer.v, (layer.attn_norm, c.norm_eps), cache, None, rope, False,
                                    slots, positions)  # fmt: skip
-            att = ops.attention(q_rot, cache, None, scale, slots, lengths, c.context, self._attention_workspace(B))
-            x = ops.linear(att, layer.o, residual=x)
+            x = ops.attention_linear(q_rot, cache, None, scale, layer.o, x, slots, lengths, c.context,
+                                     self._attention_workspace(B))  # fmt: skip
             x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))
         if last:
             x, B = x[:, -1:], 1

@@ -312,6 +312,29 @@ def attention(
     return torch.stack(outs, dim=1)
 
 
+def attention_linear(
+    q: torch.Tensor, cache: torch.Tensor, spans: list[Span] | None, scale: float, w: QTensor,
+    residual: torch.Tensor | None = None, slots=None, lengths=None, max_length: int | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:  # fmt: skip
+    """linear(attention(q, cache, ...), w, residual): an attention layer's output product
+    (leat/model.py:402-403), with the same results. On the kernel paths the attention kernels
+    write the q8 of their output themselves (kernels.attention_q8) and the product takes it as
+    it is, instead of quantizing the output again. Returns (1, T, w rows) f32."""
+    if slots is None:
+        slots, positions = _span_rows(spans)
+        lengths = [p + 1 for p in positions]
+    att_shape = (1, q.shape[2], q.shape[1] * q.shape[3])
+    # a stand-in of the attention output's shape and device, for the product's plan
+    stand_in = q.new_empty((1, 1, 1)).expand(att_shape)
+    if not reference_mode() and kernels.supports_attention(q, cache) and _plan(stand_in, w) == "decode":
+        _, q8 = kernels.attention_q8(q, cache, slots, lengths, scale, max_length, workspace)
+        (out,) = kernels.matvecs_quantized(q8, att_shape[1], att_shape[2], w, residual=residual)
+        return out.view(1, att_shape[1], w.shape[0])
+    att = attention(q, cache, None, scale, slots, lengths, max_length, workspace)
+    return linear(att, w, residual=residual)
+
+
 def argmax(x: torch.Tensor) -> torch.Tensor:
     """Each row's index of its largest value, the first one among equal values: (B, V) -> (B, 1)
     int32 (leat/ops.py:496-500)."""

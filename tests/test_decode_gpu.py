@@ -149,6 +149,43 @@ def test_attention_workspace_reuse(cuda):
             np.testing.assert_allclose(got[t], want, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("heads, kv_heads", [(32, 8), (16, 16), (16, 2)])
+def test_attention_q8_is_quantize_q8(cuda, heads, kv_heads):
+    # leat_attention_q8: the f32 output bit for bit leat_attention's, and its q8 bit for bit
+    # quantize_q8 of that output, on rows of one chunk (written by the partial kernel) and of many
+    # (by the combine), a row with no keys, and a slot outside the cache
+    rng = np.random.default_rng(heads + kv_heads)
+    n = 2048
+    cache = gpu(rng.standard_normal((2, SLOTS, kv_heads, n, 128)).astype(np.float16))
+    rows = [(0, 0), (1, 127), (2, 128), (0, 2047), (1, 600), (2, -1), (9, 10)]  # (slot, length)
+    q = gpu(normal(rng, 1, heads, len(rows), 128, scale=0.3))
+    slots, lengths = [s for s, _ in rows], [max(p, 0) for _, p in rows]
+    want = kernels.attention(q, cache, slots, lengths, 0.1, n)
+    got, (hq, hd, hs) = kernels.attention_q8(q, cache, slots, lengths, 0.1, n)
+    np.testing.assert_array_equal(host(got), host(want))
+    wq, wd, ws = kernels.quantize_q8(want.reshape(len(rows), heads * 128))
+    np.testing.assert_array_equal(host(hq), host(wq))
+    np.testing.assert_array_equal(host(hd), host(wd))
+    np.testing.assert_array_equal(host(hs), host(ws))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 8])
+def test_attention_linear_is_attention_then_linear(cuda, tokens):
+    # ops.attention_linear: the o product from the attention kernels' own q8, bit for bit the
+    # product of the attention output through ops.linear (which quantizes it again), residual in
+    rng = np.random.default_rng(70 + tokens)
+    heads, kv_heads, n = 32, 8, 1024
+    cache = gpu(rng.standard_normal((2, SLOTS, kv_heads, n, 128)).astype(np.float16))
+    wo = make_weights(GGMLType.Q4_K, 512, heads * 128, rng, synthetic=True)
+    q = gpu(normal(rng, 1, heads, tokens, 128, scale=0.3))
+    residual = gpu(normal(rng, 1, tokens, 512))
+    slots = torch.tensor([t % SLOTS for t in range(tokens)], dtype=torch.int32, device=cuda)
+    lengths = torch.tensor([1 + 131 * t for t in range(tokens)], dtype=torch.int32, device=cuda)
+    got = ops.attention_linear(q, cache, None, 0.1, wo.q, residual, slots, lengths, n)
+    att = ops.attention(q, cache, None, 0.1, slots, lengths, n)
+    np.testing.assert_array_equal(host(got), host(ops.linear(att, wo.q, residual=residual)))
+
+
 @pytest.mark.parametrize("rows, n", [(1, 128256), (5, 32000), (2, 300)])
 def test_argmax(cuda, rows, n):
     # leat's test_argmax (tests/test_kernels.py:926-933): many ties, the first must win; -inf
