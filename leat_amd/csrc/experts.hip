@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 
 // The first steps of a decode mixture in one launch (leat/kernels/experts.py:341-377: route,
 // quantize_q8 of rms_norm(x), experts_swiglu, quantize_q8 of the hidden rows). A workgroup owns
-// 32 rows of the expert of pair p = blockIdx.y (token p / used), so an expert chosen by k tokens
+// 32 (or 64) rows of the expert of pair p = blockIdx.y (token p / used), so an expert chosen by k tokens
 // is read k times: each pair's rows are streamed by workgroups of their own, which lets more
 // of them run at once than sharing a pass between members does.
 // 1. threads 0..255 load the token's x (and the norm weight) into registers before anything
@@ -195,9 +195,9 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
 //    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes x into
 //    LDS with the standalone quantizer's arithmetic (q8.h);
-// 4. each wave streams 4 rows of gate and up against the activations in registers;
-// 5. the 32 rows are one group of 32, so the workgroup writes the hidden rows' q8 words, d and s
-//    as well as (optionally) their f32 values.
+// 4. each wave streams 4 (or 8) rows of gate and up against the activations in registers;
+// 5. every 32 rows are one group of 32, so the workgroup writes the hidden rows' q8 words, d and
+//    s as well as (optionally) their f32 values.
 // MOE_WAVES waves of a workgroup: MOE_TILE rows, 4 a wave (MOE_WIDE_TILE, 8 a wave, for
 // launches of at least MOE_WIDE_PAIRS pairs, whose many workgroups then share out each one's
 // routing and quantization over twice the weights)
