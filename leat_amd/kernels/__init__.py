@@ -195,6 +195,12 @@ def matvecs_quantized(
     if residual is not None and len(ws) != 1:
         raise ValueError("matvecs adds a residual to the product of one matrix only")
     xq, xd, xs = q8
+    if any(w.shape[1] != cols for w in ws):
+        raise ValueError(f"matvecs_quantized: rows of {cols} values against matrices of {[w.shape[1] for w in ws]} columns")
+    if xq.numel() != tokens * cols // 4 or xd.numel() != tokens * cols // GROUP or xs.numel() != xd.numel():
+        raise ValueError(f"matvecs_quantized: q8 buffers not those of {tokens} rows of {cols} values")
+    if residual is not None and residual.numel() != tokens * ws[0].shape[0]:
+        raise ValueError("matvecs_quantized: the residual is not the product's shape")
     device = xq.device
     outs = [torch.empty(tokens * w.shape[0], dtype=torch.float32, device=device) for w in ws]
     if residual is None:
