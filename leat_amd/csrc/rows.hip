@@ -4,7 +4,7 @@
 // Work split: lane l of a wave owns the same tasks of every row (tasks l, l + 64, ...; a task is
 // 32 weights of Q4_K or Q6_K, 64 of Q8_0, as in blocks.h), so it loads its activation words and
 // scales into registers once and reuses them for every row the wave streams. Rows of more than
-// four turns of a wave's tasks (10240 to 32768 weights: 14336 has seven) are split by columns
+// four turns of a wave's tasks (more than 8192 weights, up to 32768: 14336 has seven) are split by columns
 // instead: each wave of a workgroup takes one turn of the same few rows (rows_split_kernel). A wave owns RPW
 // consecutive rows (of each matrix of the launch: gate and up for the GLU) and walks them one at
 // a time, the loads of the next rows (up to 4) in flight while the current row is computed. A row's sum
@@ -196,8 +196,8 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     }
 }
 
-// Long rows (more than 4 turns of a wave's tasks, up to 16: Q6_K or Q4_K rows of 10240 to 32768
-// weights, such as 11008, 13824, 14336, 18944) split by columns: wave w of the KS waves of a
+// Long rows (more than 4 turns of a wave's tasks, up to 16: Q6_K or Q4_K rows of more than 8192
+// weights, up to 32768, such as 11008, 13824, 14336, 18944) split by columns: wave w of the KS waves of a
 // workgroup takes turn w of every row, tasks 64w + lane (a last turn may be partial, and waves past
 // the row's turns idle), so each lane holds one task's activations and streams the workgroup's R
 // rows with P of them in flight; the waves' partial sums of a row meet in LDS and are added in
