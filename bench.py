@@ -331,7 +331,9 @@ def measure_decode(torch, model, steps, device, positions=(1, 4096)):
     """Config 3: the full single-stream decode step (embedding, 32 layers with RoPE + KV store and
     FlashDecoding over the cache, final norm + Q6_K head, argmax) as one HIP-graph replay, at each
     of `positions` cached positions (by default 1 and 4096: the step's token at position 0, then
-    at 4095 of a 4096-position cache). tok/s is one token per step; GB/s counts the matrices
+    at 4095 of a 4096-position cache), each replaying the graph whose length bucket covers it, as
+    the engine does (GraphStep: 128 keys, which need no FlashDecoding combine, or the whole
+    context). tok/s is one token per step; GB/s counts the matrices
     streamed (layers and head, as leat's bench does) and, for hbm_frac, the keys and values read
     too. FlashDecoding alone over the 32 layers' caches gets a roofline line of its own."""
     from leat_amd.model import GraphStep, weight_bytes
@@ -346,12 +348,12 @@ def measure_decode(torch, model, steps, device, positions=(1, 4096)):
         step.tokens.fill_(128000)
         torch.cuda.synchronize()
         for _ in range(3):
-            step.replay()
+            step.replay(max_length=pos + 1)
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(steps):
-            step.replay()
+            step.replay(max_length=pos + 1)
         end.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / steps

@@ -376,6 +376,8 @@ template <int G>
 static int attention_go(AttentionArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attention_partial_kernel<G>), dim3(a.chunks, a.kv_heads, a.rows), dim3(ATT_WAVES * 64), 0, st, a);
     if (check_launch("attention")) return -1;
+    // one chunk a row (every length at most ATT_KEYS): the partial kernel wrote every row
+    if (a.chunks == 1) return 0;
     const dim3 grid(a.rows * a.heads), block(ATT_COMBINE_WAVES * 64);
     const int span = (a.chunks + ATT_COMBINE_WAVES - 1) / ATT_COMBINE_WAVES;
     if (span <= 2)

@@ -108,7 +108,7 @@ class Engine:
             step.tokens.copy_(host[0], non_blocking=True)
             step.slots.copy_(host[1], non_blocking=True)
             step.positions.copy_(host[2], non_blocking=True)
-            step.replay()
+            step.replay(max_length=max(s.cached for s in batch) + 1)
             tokens = step.next[:k].tolist()
             for s, t in zip(batch, tokens, strict=True):
                 s.cached += 1

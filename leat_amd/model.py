@@ -218,13 +218,15 @@ class Model:
         return self._workspaces[rows]
 
     def logits(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
-               lengths: torch.Tensor | None = None, last: bool = False) -> torch.Tensor:  # fmt: skip
+               lengths: torch.Tensor | None = None, last: bool = False,
+               max_length: int | None = None) -> torch.Tensor:  # fmt: skip
         """One step of `tokens` (B,) int32, row b the token of the sequence in cache slot slots[b]
         at position positions[b] (device tensors): the logits (B, vocab) f32. Row b's keys and
         values go to its slot at its position, and it attends over positions 0..positions[b]
         (lengths, positions + 1, may be given to save the addition). Rows of one sequence's
         consecutive positions are a chunk of its prompt, each row seeing those before it; with
-        `last`, only the last row's logits are computed, (1, vocab)."""
+        `last`, only the last row's logits are computed, (1, vocab). `max_length`, if given, bounds
+        every row's length (the context otherwise): it sizes the attention launches."""
         c, w = self.config, self.weights
         B = tokens.shape[0]
         if lengths is None:
@@ -232,10 +234,11 @@ class Model:
         x = ops.embedding(tokens, w.embed).view(1, B, c.dim)
         scale = 1.0 / math.sqrt(c.head_dim)
         rope = (self.rope, c.head_dim)
+        longest = c.context if max_length is None else int(max_length)
         for layer, cache in zip(w.layers, self.cache, strict=True):
             q_rot = ops.qkv_rotate(x, layer.q, layer.k, layer.v, (layer.attn_norm, c.norm_eps), cache, None, rope, False,
                                    slots, positions)  # fmt: skip
-            x = ops.attention_linear(q_rot, cache, None, scale, layer.o, x, slots, lengths, c.context,
+            x = ops.attention_linear(q_rot, cache, None, scale, layer.o, x, slots, lengths, longest,
                                      self._attention_workspace(B))  # fmt: skip
             x = ops.feed_forward(x, layer.gate, layer.up, layer.down, (layer.ffn_norm, c.norm_eps))
         if last:
@@ -244,40 +247,68 @@ class Model:
         return logits.view(B, c.vocab)
 
     def step(self, tokens: torch.Tensor, slots: torch.Tensor, positions: torch.Tensor,
-             lengths: torch.Tensor | None = None, last: bool = False) -> torch.Tensor:  # fmt: skip
+             lengths: torch.Tensor | None = None, last: bool = False,
+             max_length: int | None = None) -> torch.Tensor:  # fmt: skip
         """The greedy next token of each row (of the last only, with `last`): argmax of logits(),
         (B,) int32."""
-        return ops.argmax(self.logits(tokens, slots, positions, lengths, last)).view(-1)
+        return ops.argmax(self.logits(tokens, slots, positions, lengths, last, max_length)).view(-1)
+
+
+# the keys FlashDecoding takes in one chunk (attention.hip ATT_KEYS): a step whose rows are all
+# this short runs no combine pass, and its partial kernel one chunk a row
+SHORT_CONTEXT = 128
 
 
 class GraphStep:
-    """A decode step of B rows captured once as a HIP graph over static device buffers `tokens`,
-    `slots` and `positions` (B,) int32, which the caller fills before replaying (building the
-    graph writes nothing to the cache); replay() runs it on whatever the buffers hold and leaves
-    the next tokens in `next`. With `advance`, the graph also moves each row on: tokens = next,
-    positions += 1, so replays decode one token after another with no host work between them."""
+    """A decode step of B rows captured as HIP graphs over static device buffers `tokens`, `slots`
+    and `positions` (B,) int32, which the caller fills before replaying (building the graphs
+    writes nothing to the cache); replay() runs a step on whatever the buffers hold and leaves the
+    next tokens in `next`. With `advance`, the graph also moves each row on: tokens = next,
+    positions += 1, so replays decode one token after another with no host work between them.
 
-    def __init__(self, model: Model, batch: int, advance: bool = True):
+    One graph is captured per length bucket (`buckets`, by default SHORT_CONTEXT, and always the
+    context), each sizing its attention launches for rows of at most that many keys: a caller
+    that knows its rows' longest length (position + 1) passes it to replay(), which runs the
+    smallest graph that covers it; without it the context's graph runs."""
+
+    def __init__(self, model: Model, batch: int, advance: bool = True, buckets: tuple[int, ...] = (SHORT_CONTEXT,)):
         device = model.weights.output.data.device
+        context = model.config.context
         self.model, self.batch = model, batch
+        self.buckets = tuple(sorted({min(int(b), context) for b in buckets if int(b) > 0} | {context}))
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.slots = torch.zeros(batch, dtype=torch.int32, device=device)
         # past the cache's positions: the eager warm-up below stores no key or value anywhere
-        self.positions = torch.full((batch,), model.config.context, dtype=torch.int32, device=device)
+        self.positions = torch.full((batch,), context, dtype=torch.int32, device=device)
         self.lengths = torch.ones(batch, dtype=torch.int32, device=device)
-        self._run(advance=False)  # once eagerly: every launch checked, and the memory pool warmed
+        for longest in self.buckets:  # once eagerly: every launch checked, and the memory pool warmed
+            self._run(False, longest)
         torch.cuda.synchronize(device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.next = self._run(advance)
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._next: dict[int, torch.Tensor] = {}
+        for longest in self.buckets:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._next[longest] = self._run(advance, longest)
+            self._graphs[longest] = graph
+        self.graph = self._graphs[context]
+        self.next = self._next[context]
 
-    def _run(self, advance: bool) -> torch.Tensor:
+    def _run(self, advance: bool, longest: int) -> torch.Tensor:
         torch.add(self.positions, 1, out=self.lengths)
-        nxt = self.model.step(self.tokens, self.slots, self.positions, self.lengths)
+        nxt = self.model.step(self.tokens, self.slots, self.positions, self.lengths, max_length=longest)
         if advance:
             self.tokens.copy_(nxt)
             self.positions.add_(1)
         return nxt
 
-    def replay(self) -> None:
-        self.graph.replay()
+    def replay(self, max_length: int | None = None) -> None:
+        """One step; `max_length`, if given, is at least every row's length (position + 1) in this
+        step, and selects the smallest graph whose bucket covers it."""
+        longest = self.buckets[-1]
+        if max_length is not None:
+            if max_length > longest:
+                raise ValueError(f"rows of {max_length} keys in a context of {longest}")
+            longest = next(b for b in self.buckets if b >= max_length)
+        self._graphs[longest].replay()
+        self.next = self._next[longest]

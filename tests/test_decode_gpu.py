@@ -273,3 +273,35 @@ def test_graph_step_replays_eager(cuda):
         tokens = nxt.clone()
     for a, b in zip(graphed.cache, eager.cache, strict=True):
         np.testing.assert_array_equal(host(a)[:, :, :, :6], host(b)[:, :, :, :6])
+
+
+def test_graph_step_length_buckets(cuda):
+    # replays that name their rows' longest length run the short-context graph (one attention
+    # chunk, no combine) up to 128 keys and the context's past it: positions 120..135 cross the
+    # boundary, every step the eager step's tokens bit for bit
+    weights = synthetic(TINY, seed=6)
+    cfg = LlamaConfig(**{**TINY.__dict__, "slots": 2})
+    graphed, eager = Model(cfg, weights), Model(cfg, weights)
+    step = GraphStep(graphed, 2)
+    assert step.buckets == (128, TINY.context)
+    rng = np.random.default_rng(8)
+    start = 120
+    prompt = rng.integers(0, TINY.vocab, (2, start)).astype(np.int32)
+    for model in (graphed, eager):  # the same cache up to position 119 in both
+        for row in range(2):
+            ids = torch.tensor(prompt[row], dtype=torch.int32, device=cuda)
+            model.step(ids, torch.full((start,), row, dtype=torch.int32, device=cuda),
+                       torch.arange(start, dtype=torch.int32, device=cuda), last=True)  # fmt: skip
+    tokens = torch.tensor([5, 9], dtype=torch.int32, device=cuda)
+    step.tokens.copy_(tokens)
+    step.slots.copy_(torch.arange(2, dtype=torch.int32))
+    step.positions.fill_(start)
+    slots = torch.arange(2, dtype=torch.int32, device=cuda)
+    for pos in range(start, start + 16):
+        step.replay(max_length=pos + 1)
+        nxt = eager.step(tokens, slots, torch.full((2,), pos, dtype=torch.int32, device=cuda))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(step.next), host(nxt), err_msg=f"position {pos}")
+        tokens = nxt.clone()
+    with pytest.raises(ValueError):
+        step.replay(max_length=TINY.context + 1)
