@@ -67,3 +67,35 @@ def test_batched_decode_matches_alone(cuda):
         assert np.abs(c[:, e.spare, :, 0]).sum() > 0 and not c[:, e.spare, :, 1:].any()
         for s in seqs:
             assert not c[:, s.slot, :, s.cached :].any()
+
+
+@pytest.mark.gpu
+def test_engine_decode_across_length_buckets(cuda):
+    # a sequence whose decode steps cross 128 positions: the engine replays the short-context
+    # graph, then the context's; every token that of eager steps sized for the whole context
+    import torch
+
+    from leat_amd.engine import Engine
+    from leat_amd.model import LlamaConfig, Model, synthetic
+
+    cfg = LlamaConfig(dim=512, layers=2, heads=8, kv_heads=2, head_dim=128, ffn=1024, vocab=1000, context=256,
+                      rope_theta=10000.0, rope_scaling=None)  # fmt: skip
+    weights = synthetic(cfg, seed=12)
+    prompt = [int(t) for t in np.random.default_rng(12).integers(0, cfg.vocab, 120)]
+    steps = 16
+    e = Engine(cfg, weights, slots=1)
+    s = e.start(prompt)
+    for _ in range(steps):
+        e.decode([s])
+    assert e._graphs[1].buckets == (128, 256)
+    model = Model(LlamaConfig(**{**cfg.__dict__, "slots": 1}), weights)
+    one = torch.zeros(1, dtype=torch.int32, device=cuda)
+    ids = torch.tensor(prompt, dtype=torch.int32, device=cuda)
+    nxt = model.step(ids, one.expand(len(prompt)).contiguous(), torch.arange(len(prompt), dtype=torch.int32, device=cuda),
+                     last=True)  # fmt: skip
+    tokens = list(prompt) + [int(nxt[-1])]
+    for pos in range(len(prompt), len(prompt) + steps):
+        nxt = model.step(torch.tensor([tokens[-1]], dtype=torch.int32, device=cuda), one,
+                         torch.tensor([pos], dtype=torch.int32, device=cuda))  # fmt: skip
+        tokens.append(int(nxt[0]))
+    assert s.tokens == tokens
