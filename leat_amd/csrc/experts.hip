@@ -195,14 +195,16 @@ __global__ __launch_bounds__(256) void experts_glu_kernel(ExpertsGluArgs a) {
 // 3. its waves issue the loads of their rows (lanes own the same tasks of every row, as in the
 //    row-streaming matvec kernels, RowTask), then the workgroup normalizes and quantizes x into
 //    LDS with the standalone quantizer's arithmetic (q8.h);
-// 4. each wave streams 4 (or 8) rows of gate and up against the activations in registers;
+// 4. each wave streams 2 (or 8) rows of gate and up against the activations in registers;
 // 5. every 32 rows are one group of 32, so the workgroup writes the hidden rows' q8 words, d and
 //    s as well as (optionally) their f32 values.
-// MOE_WAVES waves of a workgroup: MOE_TILE rows, 4 a wave (MOE_WIDE_TILE, 8 a wave, for
-// launches of at least MOE_WIDE_PAIRS pairs, whose many workgroups then share out each one's
-// routing and quantization over twice the weights)
-constexpr int MOE_WAVES = 8, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
-constexpr int MOE_WIDE_TILE = 64, MOE_WIDE_PAIRS = 32;
+// Workgroups of MOE_TILE rows in MOE_WAVES waves, 2 rows a wave; for launches of at least
+// MOE_WIDE_PAIRS pairs, whose many workgroups then share out each one's routing and quantization
+// over twice the weights, MOE_WIDE_TILE rows in MOE_WIDE_WAVES waves, 8 a wave. Measured at
+// Qwen3-30B-A3B's shape: 16 waves took the B=1 launch from 10.5 to 10.2 us and the B=8 one from
+// 24.0 to 25.9 us, hence the two widths.
+constexpr int MOE_WAVES = 16, MOE_TILE = 32, MOE_MAX_TOKENS = 8, MOE_MAX_USED = 64;
+constexpr int MOE_WIDE_TILE = 64, MOE_WIDE_WAVES = 8, MOE_WIDE_PAIRS = 32;
 
 struct MoeGluArgs {
     const uint8_t* gate;
@@ -225,17 +227,17 @@ struct MoeGluArgs {
     float* hs;
 };
 
-template <int TYPE, int NT, int EPL, int TILE>
-__global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
+template <int TYPE, int NT, int EPL, int TILE, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     using RT = RowTask<TYPE>;
-    constexpr int RPW = TILE / MOE_WAVES;
+    constexpr int RPW = TILE / WAVES;
     // rows of loads in flight: all of a narrow tile's; one of a wide tile's, whose launches of many
     // pairs keep more waves resident instead (measured fastest at 8 tokens of top-8)
     constexpr int P = NT == 1 ? (TILE == MOE_TILE ? RPW : 1) : NT == 2 ? 2 : 1;
     extern __shared__ uint32_t moe_lds[];  // the token's q8 row: words, then d, then s
     __shared__ int route_id[MOE_MAX_USED];
     __shared__ float route_w[MOE_MAX_USED];
-    __shared__ float partial[MOE_WAVES];
+    __shared__ float partial[WAVES];
     __shared__ float glu_out[TILE];
 
     const int lane = threadIdx.x & (WAVE - 1);
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     const uint8_t* u_at = a.up + (size_t)(e * a.stride + a.up_first) * row_bytes;
     typename RT::Raw rg[P][NT], ru[P][NT];
     auto fetch = [&](int slot, int r) {
-        const uint32_t at = (uint32_t)min(row0 + MOE_WAVES * r, a.rows - 1) * row_bytes;
+        const uint32_t at = (uint32_t)min(row0 + WAVES * r, a.rows - 1) * row_bytes;
 #pragma unroll
         for (int i = 0; i < NT; i++)
             if (has[i]) {
@@ -290,10 +292,10 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     for (int r = 0; r < P; r++) fetch(r, r);
     float* lds_d = (float*)(moe_lds + cols / 4);
     if constexpr (EARLY_X) {
-        xin.template quantize<MOE_WAVES * 64>(0, a.norm, a.eps, cols, partial, moe_lds, lds_d, lds_d + cols / GROUP);
+        xin.template quantize<WAVES * 64>(0, a.norm, a.eps, cols, partial, moe_lds, lds_d, lds_d + cols / GROUP);
     } else {
-        const float inv = a.norm ? block_inv_rms<MOE_WAVES * 64>(xr, cols, a.eps, partial) : 1.0f;
-        quantize_row<MOE_WAVES * 64>(xr, cols, a.norm, inv, moe_lds, lds_d, lds_d + cols / GROUP);
+        const float inv = a.norm ? block_inv_rms<WAVES * 64>(xr, cols, a.eps, partial) : 1.0f;
+        quantize_row<WAVES * 64>(xr, cols, a.norm, inv, moe_lds, lds_d, lds_d + cols / GROUP);
     }
     __syncthreads();
     ActQ act[NT];
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     // 4. the rows
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-        const int row = row0 + MOE_WAVES * r;
+        const int row = row0 + WAVES * r;
         float g = 0.0f, u = 0.0f;
 #pragma unroll
         for (int i = 0; i < NT; i++)
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
         const float ub = a.up_bias && row < a.rows ? a.up_bias[(int64_t)e * a.rows + row] : 0.0f;
         const float y = glu(a.kind, wave_sum_dpp(g) + gb, wave_sum_dpp(u) + ub);
         if (lane == 0) {
-            glu_out[w + MOE_WAVES * r] = y;
+            glu_out[w + WAVES * r] = y;
             if (a.out && row < a.rows) a.out[(int64_t)p * a.rows + row] = y;
         }
     }
@@ -348,22 +350,23 @@ __global__ __launch_bounds__(MOE_WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     }
 }
 
-template <int TYPE, int NT, int TILE>
+template <int TYPE, int NT, int TILE, int WAVES>
 static void moe_glu_tile(MoeGluArgs& a, hipStream_t st) {
     const dim3 grid(a.rows / TILE, a.tokens * a.used);
     const size_t lds = (size_t)a.cols + 2 * (size_t)(a.cols / GROUP) * 4;
     if (a.experts <= WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 1, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 1, TILE, WAVES>), grid, dim3(WAVES * 64), lds, st, a);
     else if (a.experts <= 2 * WAVE)
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 2, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 2, TILE, WAVES>), grid, dim3(WAVES * 64), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 4, TILE>), grid, dim3(MOE_WAVES * 64), lds, st, a);
+        hipLaunchKernelGGL((moe_glu_kernel<TYPE, NT, 4, TILE, WAVES>), grid, dim3(WAVES * 64), lds, st, a);
 }
 
 template <int TYPE, int NT>
 static void moe_glu_go(MoeGluArgs& a, hipStream_t st) {
-    if (a.tokens * a.used >= MOE_WIDE_PAIRS && a.rows % MOE_WIDE_TILE == 0) return moe_glu_tile<TYPE, NT, MOE_WIDE_TILE>(a, st);
-    moe_glu_tile<TYPE, NT, MOE_TILE>(a, st);
+    if (a.tokens * a.used >= MOE_WIDE_PAIRS && a.rows % MOE_WIDE_TILE == 0)
+        return moe_glu_tile<TYPE, NT, MOE_WIDE_TILE, MOE_WIDE_WAVES>(a, st);
+    moe_glu_tile<TYPE, NT, MOE_TILE, MOE_WAVES>(a, st);
 }
 
 template <int TYPE>
