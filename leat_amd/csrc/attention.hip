@@ -69,9 +69,12 @@ __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
 // --------------------------------------------------------------------------------- attention
 
 constexpr int ATT_WAVES = 8;                       // waves a workgroup
-constexpr int ATT_WAVE_KEYS = 16;                  // keys a wave takes per round
-constexpr int ATT_KEYS = ATT_WAVES * ATT_WAVE_KEYS;  // keys a workgroup takes per round
 constexpr int ATT_CHUNKS = 64;                     // most workgroups per (row, kv head): longer rows loop
+// Keys a wave takes per round: 16, or 8 for launches whose rows run past one 128-key chunk but at
+// most ATT_EIGHT_KEYS_UP_TO keys, where twice the workgroups (each with half the serial math a
+// round) finish sooner; longer rows keep 16, whose 32 or fewer chunks a row the combine gathers
+// in fewer loads a lane.
+constexpr int ATT_EIGHT_KEYS_UP_TO = 2048;
 constexpr int ATT_DIM = 128;                       // head dimension: a pair of dimensions a lane
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG = -1e30f;  // a finite floor: a fully masked wave never computes -inf - -inf
@@ -84,6 +87,7 @@ struct AttentionArgs {
     const int32_t* slots;     // rows
     const int32_t* lengths;   // rows: keys 0 .. length - 1 of the row's slot
     int chunks;               // workgroups per (row, kv head)
+    int key_bits;             // log2 of the keys a workgroup takes per round (ATT_WAVES times a wave's)
     float scale;
     float* partial;  // (rows * heads, chunks, dim + 2): unnormalized output, then max (log2 units) and sum
     float* out;      // (rows, heads * dim)
@@ -177,17 +181,18 @@ __device__ __forceinline__ float transpose_sum16(float (&v)[16], int lane) {
     return s;
 }
 
-// A workgroup per (row, kv head, chunk): its waves take ATT_WAVE_KEYS keys each a round, from key
-// chunk * ATT_KEYS + ATT_WAVE_KEYS w, then every chunks * ATT_KEYS keys on. Lane l holds dimensions 2l, 2l + 1
+// A workgroup per (row, kv head, chunk): its waves take WK keys each a round, from key
+// chunk * KEYS + WK w (KEYS = ATT_WAVES WK), then every chunks * KEYS keys on. Lane l holds dimensions 2l, 2l + 1
 // of the group's queries (scaled by scale * log2 e, so scores are in log2 units) and reads the
 // same two of each key: every key is one coalesced 256-byte read. The keys' partial dot
 // products of each lane are summed across the wave by transpose_sum16, the scores go through LDS
 // to lanes a key each for the online softmax, and the weighted values are summed with lanes
 // again a pair of dimensions (a key's values one coalesced 256-byte read). The waves merge
 // through LDS into the workgroup's partial.
-template <int G>
+template <int G, int WK>
 __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(AttentionArgs a) {
-    __shared__ float scores[ATT_WAVES][G][ATT_WAVE_KEYS];
+    constexpr int KEYS = ATT_WAVES * WK;
+    __shared__ float scores[ATT_WAVES][G][WK];
     __shared__ float merge[ATT_WAVES][G][ATT_DIM + 2];
     __shared__ float4 alone_out[G][ATT_DIM / 4];  // a single-chunk row's outputs, for their q8
     const int lane = threadIdx.x & 63;
@@ -213,16 +218,36 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
 #pragma unroll
     for (int h = 0; h < G; h++) m[h] = NEG, l[h] = 0.0f, acc[h][0] = acc[h][1] = 0.0f;
 
-    for (int base = chunk * ATT_KEYS + w * ATT_WAVE_KEYS; base < length; base += a.chunks * ATT_KEYS) {
-        // the round's keys and values are all read at once (2 ATT_WAVE_KEYS reads in flight a wave)
-        uint32_t kv[ATT_WAVE_KEYS], vv[ATT_WAVE_KEYS];
+    for (int base = chunk * KEYS + w * WK; base < length; base += a.chunks * KEYS) {
+        // the round's keys and values are all read at once (2 WK reads in flight a wave)
+        uint32_t kv[WK], vv[WK];
 #pragma unroll
-        for (int j = 0; j < ATT_WAVE_KEYS; j++) kv[j] = keys[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
+        for (int j = 0; j < WK; j++) kv[j] = keys[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
 #pragma unroll
-        for (int j = 0; j < ATT_WAVE_KEYS; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
-        // scores of keys base .. base + ATT_WAVE_KEYS - 1: 16 keys at a time, lane l's share of each dot product
+        for (int j = 0; j < WK; j++) vv[j] = vals[(int64_t)min(base + j, last) * (ATT_DIM / 2)];
+        // scores of keys base .. base + WK - 1, lane l's share of each dot product summed over the
+        // wave 16 values at a time: 8 keys of two heads (value i: head 2 hp + i / 8, key i % 8; a
+        // missing odd head adds zeros), or 16 keys of one
+        if constexpr (WK == 8) {
 #pragma unroll
-        for (int sb = 0; sb < ATT_WAVE_KEYS / 16; sb++) {
+            for (int hp = 0; hp < (G + 1) / 2; hp++) {
+                const int odd = 2 * hp + 1 < G ? 2 * hp + 1 : 2 * hp;
+                float part[16];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t kj = kv[j];
+                    const float k0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kj & 0xFFFFu));
+                    const float k1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(kj >> 16));
+                    part[j] = qa[2 * hp] * k0 + qb[2 * hp] * k1;
+                    part[8 + j] = 2 * hp + 1 < G ? qa[odd] * k0 + qb[odd] * k1 : 0.0f;
+                }
+                const float s = transpose_sum16(part, lane);
+                const int i = (lane >> 2) & 15;
+                if ((lane & 3) == 0 && 2 * hp + i / 8 < G) scores[w][i < 8 ? 2 * hp : odd][i & 7] = s;
+            }
+        }
+#pragma unroll
+        for (int sb = 0; sb < WK / 16; sb++) {
 #pragma unroll
             for (int h = 0; h < G; h++) {
                 float part[16];
@@ -237,23 +262,23 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
                 if ((lane & 3) == 0) scores[w][h][16 * sb + (lane >> 2)] = s;
             }
         }
-        // the online softmax, a key a lane (lanes ATT_WAVE_KEYS.. idle): rescale by the new maximum's step
-        const int keys_here = min(ATT_WAVE_KEYS, length - base);
+        // the online softmax, a key a lane (lanes WK.. idle): rescale by the new maximum's step
+        const int keys_here = min(WK, length - base);
         const bool valid = lane < keys_here;
 #pragma unroll
         for (int h = 0; h < G; h++) {
-            const float sc = valid ? scores[w][h][lane & (ATT_WAVE_KEYS - 1)] : NEG;
+            const float sc = valid ? scores[w][h][lane & (WK - 1)] : NEG;
             const float top = fmaxf(m[h], wave_max_dpp(sc));
             const float p = valid ? exp2f(sc - top) : 0.0f;
             const float shrink = exp2f(m[h] - top);
             m[h] = top;
             l[h] = l[h] * shrink + wave_sum_dpp(p);
             acc[h][0] *= shrink, acc[h][1] *= shrink;
-            if (lane < ATT_WAVE_KEYS) scores[w][h][lane] = p;
+            if (lane < WK) scores[w][h][lane] = p;
         }
         // weighted values: lane = dimensions 2 lane, 2 lane + 1; keys past the row weigh nothing
 #pragma unroll
-        for (int j = 0; j < ATT_WAVE_KEYS; j++) {
+        for (int j = 0; j < WK; j++) {
             // a position past the row's keys may hold anything, NaN included: it adds nothing
             const bool in = j < keys_here;
             const float v0 = in ? (float)__builtin_bit_cast(_Float16, (uint16_t)(vv[j] & 0xFFFFu)) : 0.0f;
@@ -276,7 +301,7 @@ __global__ __launch_bounds__(ATT_WAVES * 64) void attention_partial_kernel(Atten
         if (lane == 0) merge[w][h][ATT_DIM] = m[h], merge[w][h][ATT_DIM + 1] = l[h];
     }
     __syncthreads();
-    const bool alone = (length + ATT_KEYS - 1) / ATT_KEYS <= 1;  // no keys, or all in chunk 0
+    const bool alone = (length + KEYS - 1) / KEYS <= 1;  // no keys, or all in chunk 0
     if (alone && chunk != 0) return;
     for (int i = threadIdx.x; i < G * (ATT_DIM + 2); i += ATT_WAVES * 64) {
         const int h = i / (ATT_DIM + 2), d = i % (ATT_DIM + 2);
@@ -338,7 +363,7 @@ __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kern
     const int length = slot >= 0 && slot < a.cache_slots ? min(asked, a.cache_positions) : 0;
     // a row of one live chunk was written by the partial kernel's chunk 0: the workgroup runs
     // through (no branch for the loads above to sink below) and stores nothing
-    const int live = min(a.chunks, (length + ATT_KEYS - 1) / ATT_KEYS);
+    const int live = min(a.chunks, (length + (1 << a.key_bits) - 1) >> a.key_bits);
     if (lane >= live) mine = make_float2(NEG, 0.0f);
 #pragma unroll
     for (int i = 0; i < SPAN; i++)
@@ -374,9 +399,13 @@ __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kern
 
 template <int G>
 static int attention_go(AttentionArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((attention_partial_kernel<G>), dim3(a.chunks, a.kv_heads, a.rows), dim3(ATT_WAVES * 64), 0, st, a);
+    const dim3 chunks(a.chunks, a.kv_heads, a.rows), waves(ATT_WAVES * 64);
+    if (a.key_bits == 6)
+        hipLaunchKernelGGL((attention_partial_kernel<G, 8>), chunks, waves, 0, st, a);
+    else
+        hipLaunchKernelGGL((attention_partial_kernel<G, 16>), chunks, waves, 0, st, a);
     if (check_launch("attention")) return -1;
-    // one chunk a row (every length at most ATT_KEYS): the partial kernel wrote every row
+    // one chunk a row (every length at most a round's keys): the partial kernel wrote every row
     if (a.chunks == 1) return 0;
     const dim3 grid(a.rows * a.heads), block(ATT_COMBINE_WAVES * 64);
     const int span = (a.chunks + ATT_COMBINE_WAVES - 1) / ATT_COMBINE_WAVES;
@@ -391,8 +420,15 @@ static int attention_go(AttentionArgs& a, hipStream_t st) {
     return check_launch("attention combine");
 }
 
+// log2 of the keys a workgroup takes per round for rows of up to max_length keys
+static int attention_key_bits(int max_length) {
+    static_assert(ATT_WAVES == 8, "8 waves of 8 or 16 keys");
+    return max_length > ATT_WAVES * 16 && max_length <= ATT_EIGHT_KEYS_UP_TO ? 6 : 7;
+}
+
 static int attention_chunks(int max_length) {
-    return std::max(1, std::min(ATT_CHUNKS, (max_length + ATT_KEYS - 1) / ATT_KEYS));
+    const int keys = 1 << attention_key_bits(max_length);
+    return std::max(1, std::min(ATT_CHUNKS, (max_length + keys - 1) / keys));
 }
 
 }  // namespace leat
@@ -439,7 +475,8 @@ static int attention_launch(const float* q, const void* cache, int cache_slots, 
                  (long long)leat_attention_workspace(rows, heads, max_length));
     if (rows == 0) return 0;
     AttentionArgs a = {q, (const _Float16*)cache, cache_slots, kv_heads, cache_positions, rows, heads, group, slots,
-                       lengths, attention_chunks(max_length), scale, workspace, out, hq, hd, hs};
+                       lengths, attention_chunks(max_length), attention_key_bits(max_length), scale, workspace,
+                       out, hq, hd, hs};
     hipStream_t st = (hipStream_t)stream;
     switch (group) {
     case 1: return attention_go<1>(a, st);

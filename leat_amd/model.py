@@ -254,8 +254,9 @@ class Model:
         return ops.argmax(self.logits(tokens, slots, positions, lengths, last, max_length)).view(-1)
 
 
-# the keys FlashDecoding takes in one chunk (attention.hip ATT_KEYS): a step whose rows are all
-# this short runs no combine pass, and its partial kernel one chunk a row
+# the keys FlashDecoding takes in one chunk for launches of at most this many keys (8 waves of 16
+# keys, attention.hip): a step whose rows are all this short runs no combine pass, and its partial
+# kernel one chunk a row
 SHORT_CONTEXT = 128
 
 

@@ -131,6 +131,25 @@ def test_attention_rows(cuda, heads, kv_heads):
         assert_close(got[t], want, 1e-4)
 
 
+@pytest.mark.parametrize("max_length", [128, 129, 2048, 2049])
+@pytest.mark.parametrize("heads, kv_heads", [(8, 8), (8, 4), (16, 4), (16, 2)])
+def test_attention_wave_keys(cuda, heads, kv_heads, max_length):
+    # launches of 129 .. 2048 keys take 8 keys a wave (64-key chunks), the others 16 (128-key
+    # chunks): rows ending either side of both chunk sizes, in every query-group size
+    rng = np.random.default_rng(max_length + heads + kv_heads)
+    cache = rng.standard_normal((2, SLOTS, kv_heads, 2560, 128)).astype(np.float16)
+    rows = [(s, p) for s, p in [(0, 0), (1, 63), (2, 64), (0, 127), (1, 128), (2, 1000), (0, 2047), (1, 2048)]
+            if p < max_length]  # fmt: skip
+    q = normal(rng, 1, heads, len(rows), 128, scale=0.3)
+    slots, lengths = [s for s, _ in rows], [p + 1 for _, p in rows]
+    got = host(kernels.attention(gpu(q), gpu(cache), slots, lengths, 0.1, max_length))[0]
+    got = got.reshape(len(rows), heads, 128)
+    for t, (slot, pos) in enumerate(rows):
+        want = O.attention(q[0, :, t], cache[0, slot, :, : pos + 1], cache[1, slot, :, : pos + 1], 0.1)
+        np.testing.assert_allclose(got[t], want, rtol=2e-3, atol=2e-3)
+        assert_close(got[t], want, 1e-4)
+
+
 def test_attention_workspace_reuse(cuda):
     # one workspace serves calls of as many rows or fewer one after another
     rng = np.random.default_rng(5)
