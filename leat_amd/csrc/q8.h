@@ -30,8 +30,15 @@ __device__ __forceinline__ float block_inv_rms(const float* __restrict__ xr, int
     const int tid = threadIdx.x;
     float ss = 0.0f;
     if (tid < 256)
-        for (int at = tid * 4; at < n; at += 1024) {
-            ss += sum_sq4(*(const float4*)(xr + at));
+        for (int at0 = tid * 4; at0 < n; at0 += 4 * 1024) {
+            // 4 loads in flight, summed in order
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (at0 + 1024 * u < n) v[u] = *(const float4*)(xr + at0 + 1024 * u);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (at0 + 1024 * u < n) ss += sum_sq4(v[u]);
         }
     ss = wave_sum_dpp(ss);
     __syncthreads();  // `partial` may still be read from a previous row
@@ -95,15 +102,28 @@ template <int THREADS = 256, typename Q, typename F>
 __device__ __forceinline__ void quantize_row(const float* __restrict__ xr, int n, const float* __restrict__ weight,
                                              float inv, Q* q, F* d, F* s) {
     const int tid = threadIdx.x;
-    for (int at = tid * 4; at < n; at += 4 * THREADS) {  // n % 32 == 0: an octet is all in or all out
-        float4 v = *(const float4*)(xr + at);
-        if (weight) v = normed4(v, inv, *(const float4*)(weight + at));
-        float dv, sv;
-        const uint32_t word = quantize4(v, &dv, &sv);
-        q[at / 4] = word;
-        if ((tid & 7) == 0) {
-            d[at / GROUP] = dv;
-            s[at / GROUP] = sv;
+    // n % 32 == 0: an octet is all in or all out; 4 float4 (and their norm weights) in flight
+    for (int at0 = tid * 4; at0 < n; at0 += 16 * THREADS) {
+        float4 v[4], w[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int at = at0 + 4 * THREADS * u;
+            if (at < n) {
+                v[u] = *(const float4*)(xr + at);
+                if (weight) w[u] = *(const float4*)(weight + at);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int at = at0 + 4 * THREADS * u;
+            if (at >= n) break;
+            float dv, sv;
+            const uint32_t word = quantize4(weight ? normed4(v[u], inv, w[u]) : v[u], &dv, &sv);
+            q[at / 4] = word;
+            if ((tid & 7) == 0) {
+                d[at / GROUP] = dv;
+                s[at / GROUP] = sv;
+            }
         }
     }
 }
