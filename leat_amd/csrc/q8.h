@@ -187,32 +187,21 @@ struct RowsInRegs {
 };
 
 // The q8 of one group of 32 consecutive outputs per token, as quantize_q8 would write it: value i
-// of token t is vals[t][i] (shared memory), and threads 32t + i of the block (t < B) quantize it
-// into group `group` of the token's row of `rows` values (hq words, hd and hs per group).
+// of token t is vals[t][i] (shared memory, 16-byte aligned), and the aligned octet of threads
+// 8t .. 8t + 7 of the block (t < B) quantizes it with quantize4, a float4 a thread (DPP moves
+// only), into group `group` of the token's row of `rows` values (hq words, hd and hs per group).
 template <int B>
 __device__ __forceinline__ void store_group_q8(const float (*vals)[32], int rows, int group, uint32_t* hq, float* hd,
                                                float* hs) {
-    if (threadIdx.x >= 32 * B) return;
-    const int t = threadIdx.x >> 5, i = threadIdx.x & 31;
-    const float v = vals[t][i];
-    float amax = fabsf(v);
-#pragma unroll
-    for (int s = 1; s < 32; s <<= 1) amax = fmaxf(amax, __shfl_xor(amax, s, 32));
-    const float scale = amax / 127.0f;
-    const int q = scale > 0.0f ? (int)roundf(v / scale) : 0;
-    int total = q;
-#pragma unroll
-    for (int s = 1; s < 32; s <<= 1) total += __shfl_xor(total, s, 32);
-    // four consecutive lanes' values make a word, value 4w + i in byte i
-    const uint32_t b0 = (uint32_t)(q & 0xFF);
-    const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
-    const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
-    const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
-    if ((i & 3) == 0) hq[((int64_t)t * rows + 32 * group + i) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-    if (i == 0) {
-        const int64_t g = ((int64_t)t * rows + 32 * group) / GROUP;
-        hd[g] = scale;
-        hs[g] = scale * (float)total;
+    if (threadIdx.x >= 8 * B) return;
+    const int t = threadIdx.x >> 3, o = threadIdx.x & 7;
+    float dv, sv;
+    const uint32_t word = quantize4(((const float4*)vals[t])[o], &dv, &sv);
+    const int64_t first = (int64_t)t * rows + 32 * group;
+    hq[first / 4 + o] = word;
+    if (o == 0) {
+        hd[first / GROUP] = dv;
+        hs[first / GROUP] = sv;
     }
 }
 

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(WPG * 64) void rows_kernel(RowsArgs a) {
     constexpr int NM = MODE == ROWS_GLU ? 2 : 1;
     extern __shared__ uint32_t rows_lds[];
     __shared__ float partial[WPG < 4 ? 4 : WPG];
-    __shared__ float glu_out[B][32];
+    __shared__ __align__(16) float glu_out[B][32];  // float4 reads by the q8 epilogue
 
     const int cols = a.cols, tasks = cols / T::TASK_W;
     const int lane = threadIdx.x & (WAVE - 1);
