@@ -238,7 +238,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
     __shared__ int route_id[MOE_MAX_USED];
     __shared__ float route_w[MOE_MAX_USED];
     __shared__ float partial[WAVES];
-    __shared__ float glu_out[TILE];
+    __shared__ __align__(16) float glu_out[TILE];  // float4 reads by the q8 epilogue
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -323,29 +323,19 @@ __global__ __launch_bounds__(WAVES * 64) void moe_glu_kernel(MoeGluArgs a) {
         }
     }
 
-    // 5. the outputs quantized in groups of 32, a thread a row (rows a multiple of TILE)
+    // 5. the outputs quantized in groups of 32 (rows a multiple of TILE): an aligned octet of
+    // threads a group, a float4 a thread (quantize4: DPP moves only)
     if (!a.hq) return;
     __syncthreads();
-    if ((int)threadIdx.x < TILE) {
+    if ((int)threadIdx.x < TILE / 4) {
         const int i = threadIdx.x;
-        const float v = glu_out[i];
-        float amax = fabsf(v);
-#pragma unroll
-        for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
-        const float scale = amax / 127.0f;
-        const int q = scale > 0.0f ? (int)roundf(v / scale) : 0;
-        int total = q;
-#pragma unroll
-        for (int sft = 1; sft < 32; sft <<= 1) total += __shfl_xor(total, sft, 32);
-        const uint32_t b0 = (uint32_t)(q & 0xFF);
-        const uint32_t b1 = (uint32_t)__shfl_down((int)b0, 1, 32);
-        const uint32_t b2 = (uint32_t)__shfl_down((int)b0, 2, 32);
-        const uint32_t b3 = (uint32_t)__shfl_down((int)b0, 3, 32);
-        const int64_t first = (int64_t)p * a.rows + row_base + (i & ~31);  // the group's first row
-        if ((i & 3) == 0) a.hq[(first + (i & 31)) / 4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        if ((i & 31) == 0) {
-            a.hd[first / GROUP] = scale;
-            a.hs[first / GROUP] = scale * (float)total;
+        float dv, sv;
+        const uint32_t word = quantize4(((const float4*)glu_out)[i], &dv, &sv);
+        const int64_t first = (int64_t)p * a.rows + row_base;  // the tile's first row: a group boundary
+        a.hq[first / 4 + i] = word;
+        if ((i & 7) == 0) {
+            a.hd[first / GROUP + i / 8] = dv;
+            a.hs[first / GROUP + i / 8] = sv;
         }
     }
 }

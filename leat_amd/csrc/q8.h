@@ -96,6 +96,39 @@ __device__ __forceinline__ uint32_t quantize4(float4 v, float* d_out, float* s_o
            ((uint32_t)(q3 & 0xFF) << 24);
 }
 
+// v of each lane combined with `op` over its aligned 32 lanes, by DPP moves and the gfx950
+// permlane16 swap (no LDS traffic): xor 1, 2, 4 as octet_reduce, xor 8 as a rotation of the row
+// of 16 by 8, then the two rows of 16 exchanged (each lane gets its own value and its partner's,
+// in an order that depends on the lane: op must commute)
+template <typename Op>
+__device__ __forceinline__ float lane32_reduce(float v, Op op) {
+    v = octet_reduce(v, op);
+    v = op(v, LEAT_DPP(v, 0x128, 0xF, 0xF));  // row_ror:8
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const uint32_t lo = r[0], hi = r[1];
+    return op(__uint_as_float(lo), __uint_as_float(hi));
+}
+
+// The q8 of a group of 32 values held one a lane by an aligned 32 lanes of a wave (all of them
+// active), bit for bit as quantize4 and the standalone quantizer write it: returns, for lanes
+// 4j of the group, the word of the values of lanes 4j .. 4j + 3 (other lanes: unspecified); every
+// lane gets the group's d and s.
+__device__ __forceinline__ uint32_t quantize_lane32(float v, float* d_out, float* s_out) {
+    const float amax = lane32_reduce(fabsf(v), [](float a, float b) { return fmaxf(a, b); });
+    const float scale = amax / 127.0f;
+    const int q = scale > 0.0f ? round_quotient(v, scale, __builtin_amdgcn_rcpf(scale)) : 0;
+    // small integers, exact in f32 whatever the order
+    const float total = lane32_reduce((float)q, [](float a, float b) { return a + b; });
+    *d_out = scale;
+    *s_out = scale * total;
+    // lanes 4j take the bytes of lanes 4j + 1 .. 4j + 3 (row_shl:k reads lane l + k within the row of 16)
+    const int b0 = q & 0xFF;
+    const int b1 = __builtin_amdgcn_update_dpp(0, b0, 0x101, 0xF, 0xF, false);
+    const int b2 = __builtin_amdgcn_update_dpp(0, b0, 0x102, 0xF, 0xF, false);
+    const int b3 = __builtin_amdgcn_update_dpp(0, b0, 0x103, 0xF, 0xF, false);
+    return (uint32_t)b0 | ((uint32_t)b1 << 8) | ((uint32_t)b2 << 16) | ((uint32_t)b3 << 24);
+}
+
 // One row of n values (after RMSNorm when `weight` is set, `inv` its 1/rms) into q words, d and s
 // (pointers to the row's first word and group), by a block of THREADS threads. Any address space.
 template <int THREADS = 256, typename Q, typename F>

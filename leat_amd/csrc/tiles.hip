@@ -25,6 +25,7 @@
 // The GLU can also quantize its own outputs (the tile's 32 rows are one group of 32 per token)
 // for the down product, as the one- and two-token kernels do.
 #include "blocks.h"
+#include "q8.h"
 #include "tiles.h"
 
 namespace leat {
@@ -239,25 +240,14 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
 #pragma unroll
         for (int v = 0; v < TV; v++) {
             const int t = 8 * (v / 4) + 4 * h + v % 4;
-            float amax = fabsf(y[v]);
-#pragma unroll
-            for (int sft = 1; sft < 32; sft <<= 1) amax = fmaxf(amax, __shfl_xor(amax, sft, 32));
-            const float scale = amax / 127.0f;
-            const int q = scale > 0.0f ? (int)roundf(y[v] / scale) : 0;
-            int total = q;
-#pragma unroll
-            for (int sft = 1; sft < 32; sft <<= 1) total += __shfl_xor(total, sft, 32);
-            const uint32_t b0q = (uint32_t)(q & 0xFF);
-            const uint32_t b1q = (uint32_t)__shfl_down((int)b0q, 1, 32);
-            const uint32_t b2q = (uint32_t)__shfl_down((int)b0q, 2, 32);
-            const uint32_t b3q = (uint32_t)__shfl_down((int)b0q, 3, 32);
+            float scale, sum;
+            const uint32_t word = quantize_lane32(y[v], &scale, &sum);
             if (t < tokens) {
-                if ((r & 3) == 0)
-                    a.hq[((int64_t)t * rows + row0 + r) / 4] = b0q | (b1q << 8) | (b2q << 16) | (b3q << 24);
+                if ((r & 3) == 0) a.hq[((int64_t)t * rows + row0 + r) / 4] = word;
                 if (r == 0) {
                     const int64_t g = ((int64_t)t * rows + row0) / GROUP;
                     a.hd[g] = scale;
-                    a.hs[g] = scale * (float)total;
+                    a.hs[g] = sum;
                 }
             }
         }
