@@ -176,8 +176,8 @@ __device__ __forceinline__ float transpose_sum16(float (&v)[16], int lane) {
     dpp_step<2, 8>(v, lane);
     dpp_step<1, 4>(v, lane);
     float s = v[0];
-    s += __shfl_xor(s, 1, WAVE);
-    s += __shfl_xor(s, 2, WAVE);
+    s += LEAT_DPP(s, 0xB1, 0xF, 0xF);  // quad_perm [1,0,3,2]: lane ^ 1
+    s += LEAT_DPP(s, 0x4E, 0xF, 0xF);  // quad_perm [2,3,0,1]: lane ^ 2
     return s;
 }
 

@@ -78,10 +78,36 @@ __device__ __forceinline__ void load16_even(const uint8_t* base, uint64_t off, u
     out[3] = align_bytes(e, a[3], shift);
 }
 
+// The xor butterfly over the wave's 64 lanes (partners 32, 16, 8, 4, 2, 1 lanes apart, in that
+// order), every lane ending with the sum, by gfx950's permlane32 / permlane16 swaps and DPP moves
+// instead of shuffles (no LDS traffic). Each step adds the partner's value to the lane's own, the
+// shuffle butterfly's arithmetic, so sums are bit for bit the same; all 64 lanes must be active.
+// T: a 32-bit type.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, WAVE);
+    static_assert(sizeof(T) == 4, "32-bit values");
+    auto bits = [](T x) { return __builtin_bit_cast(uint32_t, x); };
+    auto val = [](uint32_t x) { return __builtin_bit_cast(T, x); };
+    {
+        // lanes with the step's bit clear get (own, partner), those with it set (partner, own)
+        const auto r = __builtin_amdgcn_permlane32_swap(bits(v), bits(v), false, false);
+        const uint32_t lo = r[0], hi = r[1];
+        v = val(lo) + val(hi);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(bits(v), bits(v), false, false);
+        const uint32_t lo = r[0], hi = r[1];
+        v = val(lo) + val(hi);
+    }
+    v += val((uint32_t)__builtin_amdgcn_update_dpp(0, (int)bits(v), 0x128, 0xF, 0xF, false));  // row_ror:8 (lane ^ 8)
+    {
+        // lane ^ 4: row_shl:4 into banks 0 and 2, row_shr:4 into banks 1 and 3
+        int other = __builtin_amdgcn_update_dpp((int)bits(v), (int)bits(v), 0x104, 0xF, 0x5, false);
+        other = __builtin_amdgcn_update_dpp(other, (int)bits(v), 0x114, 0xF, 0xA, false);
+        v += val((uint32_t)other);
+    }
+    v += val((uint32_t)__builtin_amdgcn_update_dpp(0, (int)bits(v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v += val((uint32_t)__builtin_amdgcn_update_dpp(0, (int)bits(v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
     return v;
 }
 
