@@ -161,19 +161,42 @@ __global__ __launch_bounds__(S * 64) void tiles_kernel(TileArgs a) {
     wr[0] = (MODE == TILES_GLU ? a.w[0] : a.w[m]) + (size_t)row * row_bytes;
     if (NM == 2) wr[NM - 1] = a.w[1] + (size_t)row * row_bytes;
 
-    // the wave's blocks w, w + S, ..., and the first one's loads before anything else
-    typename TB::Raw cur[NM];
-    if (w < nb)
+    // The tokens' scale tables go into LDS group-major, read in the source's order (token-major).
+    // Their first TABLE_U entries a thread are asked for first, at clamped indices, then the
+    // wave's first block of weights (blocks w, w + S, ...; a block index clamped into the row),
+    // all unconditionally: the LDS writes then wait for the table alone (the compiler counts the
+    // weight loads still in flight) and the barrier passes while the weights arrive.
+    constexpr int TABLE_U = 4;
+    const int entries = TOK * G, live_entries = tokens * G;
+    float td[TABLE_U], ts[TABLE_U];
 #pragma unroll
-        for (int k = 0; k < NM; k++) cur[k] = TB::load(wr[k], w, h);
+    for (int u = 0; u < TABLE_U; u++) {
+        const int i = min((int)threadIdx.x + u * S * 64, live_entries - 1);
+        td[u] = a.xd[i];
+        ts[u] = a.xs[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the table's loads stay ahead of the weights'
+    typename TB::Raw cur[NM];
+#pragma unroll
+    for (int k = 0; k < NM; k++) cur[k] = TB::load(wr[k], min(w, nb - 1), h);
 
-    // the tokens' scale tables into LDS, group-major: read in the source's order (token-major)
     TileActs x;
     x.d_off = 0;
     x.s_off = TOK * G;
     {
         float* tab = (float*)tiles_lds;
-        for (int i = threadIdx.x; i < TOK * G; i += S * 64) {
+#pragma unroll
+        for (int u = 0; u < TABLE_U; u++) {
+            const int i = (int)threadIdx.x + u * S * 64;
+            if (i < entries) {
+                const int t = i / G, g = i - t * G;
+                const bool in = t < tokens;
+                tab[TOK * g + t] = in ? td[u] : 0.0f;
+                tab[TOK * G + TOK * g + t] = in ? ts[u] : 0.0f;
+            }
+        }
+        // tables longer than TABLE_U entries a thread (rows of more than 4096 weights at 16 tokens)
+        for (int i = threadIdx.x + TABLE_U * S * 64; i < entries; i += S * 64) {
             const int t = i / G, g = i - t * G;
             const bool in = t < tokens;
             tab[TOK * g + t] = in ? a.xd[i] : 0.0f;
