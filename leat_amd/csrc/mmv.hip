@@ -392,45 +392,67 @@ void mmv_kernel(MmvArgs args) {
     // the wave's stages ka + ks j, j < nk: every S-th of the part's, so the S waves read
     // neighbouring blocks of the tile's rows at a time
     const int ka = p0 + wave, ks = S, nk = ka < p0 + pn ? (p0 + pn - ka + S - 1) / S : 0;
-    // MMV_DEPTH stages in flight
-    Stage<TYPE> st[MMV_DEPTH][NM];
-#pragma unroll
-    for (int p = 0; p < MMV_DEPTH; p++)
-        if (p < nk)
-#pragma unroll
-            for (int i = 0; i < NM; i++) stage_load<TYPE>(st[p][i], wm[i], row_bytes, row0, rows, ka + ks * p, lane);
-
     // operand sets: 2 (prefetched) for Q6_K's 3+ tokens outside the GLU; none (loaded when used)
     // where the register budget is 128 (occupancy 4); else 1
     using A = Acts<NV, XQ,
                    TYPE == Q6_K && NV >= 4 && MODE != MMV_GLU ? 2 : mmv_occupancy(TYPE, MODE, NV) >= 4 ? 0 : 1>;
     constexpr int TP = A::TP;
+    // The scales of the groups of the workgroup's blocks go into LDS, U loads in flight per thread.
+    // The first U a thread are asked for before anything else, at clamped indices, then the first
+    // MMV_DEPTH stages of weights (stage indices clamped into the row), all unconditionally: the
+    // table's LDS writes then wait for the table alone, counting the weight loads still in flight.
+    constexpr int GPS = TYPE == Q8_0 ? 2 : 8;  // groups a stage
+    constexpr int U = NV >= 4 ? 8 : 2;
+    const int gb0 = p0 * GPS, n = pn * GPS * TP;
+    float vd[U], vs[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int i = (int)threadIdx.x + u * (int)blockDim.x;
+        const int at = min(i % TP, tokens - 1) * G_ + min(gb0 + i / TP, G_ - 1);
+        vd[u] = args.xd[at];
+        vs[u] = TYPE == Q4_K ? args.xs[at] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the table's loads stay ahead of the weights'
+    // MMV_DEPTH stages in flight (a wave with fewer stages loads stages it never uses)
+    Stage<TYPE> st[MMV_DEPTH][NM];
+#pragma unroll
+    for (int p = 0; p < MMV_DEPTH; p++)
+#pragma unroll
+        for (int i = 0; i < NM; i++)
+            stage_load<TYPE>(st[p][i], wm[i], row_bytes, row0, rows, min(ka + ks * p, stages - 1), lane);
+
     A acts;
     acts.q = (const uint32_t*)args.xq;
     acts.cols = cols;
     acts.s_off = G_ * TP;
     acts.xq_off = table_bytes<TYPE, NV>(cols) / 4;
     {
-        // the scales of the groups of the workgroup's blocks, U loads in flight per thread
         float* tab = (float*)mmv_lds;
-        constexpr int GPS = TYPE == Q8_0 ? 2 : 8;  // groups a stage
-        const int gb0 = p0 * GPS, n = pn * GPS * TP;
-        constexpr int U = NV >= 4 ? 8 : 2;
-        for (int base = threadIdx.x; base < n; base += U * blockDim.x) {
-            float vd[U], vs[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = (int)threadIdx.x + u * (int)blockDim.x;
+            if (i < n) {
+                const bool in = i % TP < tokens;
+                tab[gb0 * TP + i] = in ? vd[u] : 0.0f;
+                if (TYPE == Q4_K) tab[(G_ + gb0) * TP + i] = in ? vs[u] : 0.0f;
+            }
+        }
+        // tables longer than U entries a thread
+        for (int base = threadIdx.x + U * blockDim.x; base < n; base += U * blockDim.x) {
+            float rd[U], rs[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = base + u * (int)blockDim.x, g = gb0 + i / TP, tk = i % TP;
                 const bool in = i < n && tk < tokens;
-                vd[u] = in ? args.xd[tk * G_ + g] : 0.0f;
-                vs[u] = TYPE == Q4_K && in ? args.xs[tk * G_ + g] : 0.0f;
+                rd[u] = in ? args.xd[tk * G_ + g] : 0.0f;
+                rs[u] = TYPE == Q4_K && in ? args.xs[tk * G_ + g] : 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = base + u * (int)blockDim.x;
                 if (i < n) {
-                    tab[gb0 * TP + i] = vd[u];
-                    if (TYPE == Q4_K) tab[(G_ + gb0) * TP + i] = vs[u];
+                    tab[gb0 * TP + i] = rd[u];
+                    if (TYPE == Q4_K) tab[(G_ + gb0) * TP + i] = rs[u];
                 }
             }
         }
