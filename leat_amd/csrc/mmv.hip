@@ -412,7 +412,14 @@ void mmv_kernel(MmvArgs args) {
         vd[u] = args.xd[at];
         vs[u] = TYPE == Q4_K ? args.xs[at] : 0.0f;
     }
-    __builtin_amdgcn_sched_barrier(0);  // the table's loads stay ahead of the weights'
+    // staged words (XQ): their first V u32x4 a thread likewise
+    constexpr int V = NV >= 4 ? 4 : 1;
+    const int quads = XQ ? tokens * (cols / 4) / 4 : 1;
+    u32x4 wq[XQ ? V : 1];
+    if constexpr (XQ)
+#pragma unroll
+        for (int u = 0; u < V; u++) wq[u] = ((const u32x4*)args.xq)[min((int)threadIdx.x + u * (int)blockDim.x, quads - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // the table's (and words') loads stay ahead of the weights'
     // MMV_DEPTH stages in flight (a wave with fewer stages loads stages it never uses)
     Stage<TYPE> st[MMV_DEPTH][NM];
 #pragma unroll
@@ -456,20 +463,24 @@ void mmv_kernel(MmvArgs args) {
                 }
             }
         }
-        if (XQ) {
-            const int words = tokens * (cols / 4);
-            constexpr int V = NV >= 4 ? 4 : 1;
-            for (int base = threadIdx.x; base < words / 4; base += V * blockDim.x) {
+        if constexpr (XQ) {
+            u32x4* staged = (u32x4*)(mmv_lds + acts.xq_off);
+#pragma unroll
+            for (int u = 0; u < V; u++) {
+                const int i = (int)threadIdx.x + u * (int)blockDim.x;
+                if (i < quads) staged[i] = wq[u];
+            }
+            for (int base = threadIdx.x + V * blockDim.x; base < quads; base += V * blockDim.x) {
                 u32x4 v[V];
 #pragma unroll
                 for (int u = 0; u < V; u++) {
                     const int i = base + u * (int)blockDim.x;
-                    if (i < words / 4) v[u] = ((const u32x4*)args.xq)[i];
+                    if (i < quads) v[u] = ((const u32x4*)args.xq)[i];
                 }
 #pragma unroll
                 for (int u = 0; u < V; u++) {
                     const int i = base + u * (int)blockDim.x;
-                    if (i < words / 4) ((u32x4*)(mmv_lds + acts.xq_off))[i] = v[u];
+                    if (i < quads) staged[i] = v[u];
                 }
             }
         }
