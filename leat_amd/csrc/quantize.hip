@@ -6,7 +6,7 @@
 //
 // A block of 256 threads per 1024 values of a row (a grid of rows x parts, so a decode step's
 // few rows still spread over many CUs); each thread takes 4 consecutive values, so the 8 lanes
-// of an aligned octet hold one group and reduce it with shuffles.
+// of an aligned octet hold one group and reduce it with DPP moves (quantize4).
 #include "q8.h"
 
 namespace leat {
