@@ -373,7 +373,8 @@ __global__ __launch_bounds__(ATT_COMBINE_WAVES * 64) void attention_combine_kern
     float y0 = 0.0f, y1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < SPAN; i++) {
-        const float fc = __shfl(f, w + ATT_COMBINE_WAVES * i, WAVE);
+        // chunk w + ATT_COMBINE_WAVES i's weight, from its lane: a wave-uniform lane index (readlane)
+        const float fc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), w + ATT_COMBINE_WAVES * i));
         y0 += fc * v[i].x, y1 += fc * v[i].y;
     }
     if (w > 0) sums[w - 1][lane] = make_float2(y0, y1);
