@@ -454,8 +454,17 @@ extern "C" int leat_rotate(const float* q, const float* k, const float* v, int t
     return check_launch("rotate");
 }
 
+// Chunks a workspace for rows of at most max_length keys holds: the most that any launch of up to
+// max_length keys takes, since launches of 8-key rounds take more chunks than some longer ones
+// (2048 keys 32, 2049 keys 17), and a workspace serves every shorter launch.
+static int attention_workspace_chunks(int max_length) {
+    return max_length > ATT_EIGHT_KEYS_UP_TO
+               ? std::max(attention_chunks(max_length), attention_chunks(ATT_EIGHT_KEYS_UP_TO))
+               : attention_chunks(max_length);
+}
+
 extern "C" int64_t leat_attention_workspace(int rows, int heads, int max_length) {
-    return (int64_t)rows * heads * attention_chunks(max_length) * (ATT_DIM + 2) * 4;
+    return (int64_t)rows * heads * attention_workspace_chunks(max_length) * (ATT_DIM + 2) * 4;
 }
 
 static int attention_launch(const float* q, const void* cache, int cache_slots, int kv_heads, int cache_positions,

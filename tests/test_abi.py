@@ -91,3 +91,12 @@ def test_binding_argument_counts_match_the_header():
     for name, args in _lib.SIGNATURES.items():
         assert name in counts, f"{name} is bound but not declared"
         assert len(args) == counts[name], name
+
+
+def test_attention_workspace_serves_shorter_launches(lib):
+    # a workspace for rows of at most L keys serves every launch of fewer keys: its size never
+    # shrinks as L grows, although launches of 129..2048 keys take 64-key chunks and longer ones
+    # 128-key chunks (2048 keys: 32 chunks, 2049: 17)
+    sizes = [lib.leat_attention_workspace(3, 32, n) for n in range(1, 9000, 7)]
+    assert all(a <= b for a, b in zip(sizes, sizes[1:]))
+    assert lib.leat_attention_workspace(1, 1, 2049) >= lib.leat_attention_workspace(1, 1, 2048)

@@ -168,6 +168,25 @@ def test_attention_workspace_reuse(cuda):
             np.testing.assert_allclose(got[t], want, rtol=2e-3, atol=2e-3)
 
 
+def test_attention_workspace_for_longer_rows(cuda):
+    # a workspace sized for rows of up to 3000 keys (128-key chunks) serves launches of 2048, 1000
+    # and 129 keys, which take more, shorter chunks
+    rng = np.random.default_rng(9)
+    heads, kv_heads, n = 16, 4, 3000
+    cache = rng.standard_normal((2, SLOTS, kv_heads, n, 128)).astype(np.float16)
+    device_cache = gpu(cache)
+    work = kernels.attention_workspace(2, heads, n, cuda)
+    for max_length, rows in ((2048, [(0, 2047), (1, 700)]), (1000, [(2, 999)]), (129, [(1, 128), (0, 3)]),
+                             (3000, [(0, 2999), (2, 64)])):  # fmt: skip
+        q = normal(rng, 1, heads, len(rows), 128, scale=0.3)
+        slots, lengths = [s for s, _ in rows], [p + 1 for _, p in rows]
+        got = host(kernels.attention(gpu(q), device_cache, slots, lengths, 0.1, max_length, work))[0]
+        got = got.reshape(len(rows), heads, 128)
+        for t, (slot, pos) in enumerate(rows):
+            want = O.attention(q[0, :, t], cache[0, slot, :, : pos + 1], cache[1, slot, :, : pos + 1], 0.1)
+            np.testing.assert_allclose(got[t], want, rtol=2e-3, atol=2e-3)
+
+
 @pytest.mark.parametrize("heads, kv_heads", [(32, 8), (16, 16), (16, 2)])
 def test_attention_q8_is_quantize_q8(cuda, heads, kv_heads):
     # leat_attention_q8: the f32 output bit for bit leat_attention's, and its q8 bit for bit
